@@ -1,0 +1,213 @@
+/*
+ * mxfp4hip.h - C ABI of libmxfp4hip, the MI355X (gfx950) MXFP4 MLP library.
+ *
+ * Drop-in boundary for the reference's MXFP4 MLP hot path
+ * (Anemll/MPP-4.1-FP4-FP8-block).  The reference binds its kernels through
+ * Metal: positional buffers 0..6 (MXFP4Kernels.metal:108-115, 264-286),
+ * encoded by main.swift helpers (encodeMXFP4MatmulDispatch main.swift:2137,
+ * encodeMXFP4FusedMLP :2033, encodeMXFP4DequantMLP :2426, encodeMPPMLP
+ * :2636).  Each entry point below names the reference interface it replaces.
+ *
+ * Conventions
+ *   - Plain C types only; device pointers come from mx_alloc (or any HIP
+ *     allocation on the context's device).  Host pointers are marked "host".
+ *   - Every function returns an mx_status; mx_last_error(ctx) holds the
+ *     message (mirrors ProbeError, main.swift:5-38).  No exceptions cross
+ *     the ABI.
+ *   - One context = one device + one HIP stream.  Launch functions are
+ *     asynchronous in stream order; *_roundtrip, mx_download, mx_sync and
+ *     the benchmark entry points are synchronous.  A context is not
+ *     thread-safe; use one per host thread.
+ *   - Layouts are the reference's (GUIDE:43-55): activations [T][K]
+ *     row-major; weights [N][K] with K contiguous; MXFP4 data [N][K/2]
+ *     (low nibble = even k), E8M0 scales [N][K/32].
+ */
+#ifndef MXFP4HIP_H
+#define MXFP4HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: ProbeError cases (main.swift:5-38). */
+typedef enum {
+  MX_OK = 0,
+  MX_EINVAL = 1,    /* invalidArgument                         */
+  MX_ENODEV = 2,    /* missingDevice                           */
+  MX_ENOKERNEL = 3, /* missingFunction / missingShaderResource */
+  MX_ENOMEM = 4,    /* missingBuffer                           */
+  MX_EGPU = 5       /* gpuExecutionFailed / missingCommand*    */
+} mx_status;
+
+/* Element types. */
+enum { MX_DTYPE_F32 = 0, MX_DTYPE_F16 = 1, MX_DTYPE_I8 = 2, MX_DTYPE_I32 = 3, MX_DTYPE_U8 = 4 };
+
+/* Packed numeric formats of the roundtrip probe (PackedNumericKernels.metal:35-96). */
+enum { MX_FMT_FP4_E2M1 = 0, MX_FMT_FP8_E4M3 = 1, MX_FMT_FP8_E5M2 = 2 };
+
+/* MLP variants (rows of runMLPBenchmark, main.swift:1043-1243). */
+enum {
+  /* fused: FP4 weights dequantized in registers by v_cvt_scalef32_pk_f16_fp4
+   * feeding fp16 MFMA, gate+up+SwiGLU in one kernel, mid f16, then down;
+   * counterpart of the native scale-plane rows (MXFP4Kernels.metal:138-173). */
+  MX_MLP_FUSED = 0,
+  /* dequant: 3 x dequant-to-half, h_h_f gate/up, swiglu_float, down
+   * (encodeMXFP4DequantMLP main.swift:2426-2538). */
+  MX_MLP_DEQUANT = 1,
+  /* W4A4: x and mid quantized to MXFP4 along K, FP4 x FP4 scaled MFMA
+   * (v_mfma_scale_f32_32x32x64_f8f6f4), fp16 out. */
+  MX_MLP_W4A4 = 2,
+  /* reference fused-row epilogue: swiglu_half (x1/16, clamp +-20, mid half),
+   * f32 out (encodeMXFP4FusedMLP main.swift:2033-2135 + MPPMLPKernels.metal:204-220);
+   * reproduces the reference checksum 403573 (README.md:292-294). */
+  MX_MLP_REFROW = 3
+};
+
+/* Weight-format rows (MPP/NAX rows main.swift:945-1042, 1247-1413;
+ * BASELINE configs[3] adds the scales). */
+enum {
+  MX_WFMT_FP8_E4M3 = 1, /* [N][K] E4M3 + f32 row scale [N] (amax/448)   */
+  MX_WFMT_FP8_E5M2 = 2, /* [N][K] E5M2 + f32 row scale [N] (amax/57344) */
+  MX_WFMT_INT8 = 3,     /* [N][K] int8 + f32 row scale [N] (amax/127)   */
+  MX_WFMT_INT4 = 4,     /* [N][K/2] int4 (low nibble = even k) + f16 scale [N][K/32] (amax/7) */
+  MX_WFMT_W8A8 = 5      /* int8 weights as MX_WFMT_INT8, int8 activations per token, i32 accumulate */
+};
+
+/* MLPConfig (main.swift:62-66, MPPMLPKernels.metal:8-12). */
+typedef struct {
+  uint32_t tokens;
+  uint32_t hidden;
+  uint32_t intermediate;
+} mx_mlp_config;
+
+/* One quantized weight matrix: data + scales (device pointers). */
+typedef struct {
+  const void* data;
+  const void* scales;
+} mx_qmatrix;
+
+/* gate [I][H], up [I][H], down [H][I]. */
+typedef struct {
+  mx_qmatrix gate, up, down;
+} mx_mlp_weights;
+
+typedef struct mx_ctx mx_ctx;
+
+/* ---- context (MTLCreateSystemDefaultDevice main.swift:91, makeQueue :193) */
+int mx_create(int device, mx_ctx** out);
+void mx_destroy(mx_ctx* ctx);
+const char* mx_last_error(const mx_ctx* ctx);
+/* Static message for a status code (usable without a context). */
+const char* mx_status_string(int status);
+/* Device name and compute-unit count ("Device: ..." main.swift:95). */
+int mx_device_info(mx_ctx* ctx, char* name_out, size_t name_len, int* cu_count, int* clock_mhz);
+/* Use the caller's HIP stream (hipStream_t as void*); NULL = context stream. */
+int mx_set_stream(mx_ctx* ctx, void* stream);
+void* mx_get_stream(mx_ctx* ctx);
+int mx_sync(mx_ctx* ctx);
+
+/* ---- device memory (device.makeBuffer, main.swift:219, 640-917) --------- */
+int mx_alloc(mx_ctx* ctx, size_t bytes, void** dptr);
+int mx_free(mx_ctx* ctx, void* dptr);
+int mx_upload(mx_ctx* ctx, void* dst, const void* host_src, size_t bytes);
+int mx_download(mx_ctx* ctx, void* host_dst, const void* src, size_t bytes);
+int mx_memset(mx_ctx* ctx, void* dst, int value, size_t bytes);
+
+/* ---- codecs --------------------------------------------------------------- */
+/* Pack/unpack roundtrip of host vectors: replaces run(testCase:) +
+ * fp4_e2m1_roundtrip / fp8_e4m3_roundtrip / fp8_e5m2_roundtrip
+ * (main.swift:202-292, PackedNumericKernels.metal:35-96).  host_packed gets
+ * n/2 (FP4) or n (FP8) bytes; host_out gets the n unpacked floats. */
+int mx_roundtrip(mx_ctx* ctx, int fmt, const float* host_in, size_t n, uint8_t* host_packed,
+                 float* host_out);
+/* Bulk device pack / unpack with the same semantics. */
+int mx_pack(mx_ctx* ctx, int fmt, const float* in, size_t n, uint8_t* packed);
+int mx_unpack(mx_ctx* ctx, int fmt, const uint8_t* packed, size_t n, float* out);
+
+/* MXFP4 block quantizer (no reference kernel: the
+ * reference generates codes directly, main.swift:633-638).  src [rows][k]
+ * f32 or f16; k % 32 == 0. */
+int mx_mxfp4_quantize(mx_ctx* ctx, const void* src, int src_dtype, int rows, int k,
+                      uint8_t* packed, uint8_t* scales);
+
+/* Dequant to half: mxfp4_dequant_native_half / mxfp4_dequant_lut_half
+ * (MXFP4Kernels.metal:509-564; ABI packed, scales, out, rows, depth). */
+int mx_mxfp4_dequant_f16(mx_ctx* ctx, const uint8_t* packed, const uint8_t* scales, void* out,
+                         int rows, int depth);
+
+/* ---- matmuls -------------------------------------------------------------- */
+/* C[m][n] = sum_k A[m][k] * fp4(B[n][k]) * 2^(S[n][k/32]-127):
+ * mxfp4_native_sp_h_f_n64 / mxfp4_fused_h_f_n64 (MXFP4Kernels.metal:108-130,
+ * 264-286; ABI a, b, c, m, n, k, scales).  a f16; c f32 or f16. */
+int mx_mxfp4_matmul(mx_ctx* ctx, const void* a, int a_dtype, const uint8_t* b, void* c,
+                    int c_dtype, int m, int n, int k, const uint8_t* scales);
+/* C f32 = A * B^T with B f16 [n][k]: mpp_mlp_h_h_f_n128 (a f16) and
+ * mpp_mlp_f_h_f_n128 (a f32) (MPPMLPKernels.metal:39-48, 164-173). */
+int mx_gemm_f16(mx_ctx* ctx, const void* a, int a_dtype, const void* b, float* c, int m, int n,
+                int k);
+/* SwiGLU: variant 0 mpp_mlp_swiglu_float, 1 mpp_mlp_swiglu_half,
+ * 2 mpp_mlp_swiglu_half_from_half, 3 mpp_mlp_swiglu_i8
+ * (MPPMLPKernels.metal:186-257; ABI gate, up, mid, config). */
+int mx_swiglu(mx_ctx* ctx, int variant, const void* gate, const void* up, void* mid, int tokens,
+              int intermediate);
+
+/* ---- MLP ------------------------------------------------------------------ */
+/* down(silu(gate(x)) * up(x)).  x f16 [T][H]; weights MXFP4; out f16 [T][H]
+ * (f32 for MX_MLP_REFROW).  Validation as runMLPBenchmark (main.swift:592-597):
+ * positive sizes, hidden/intermediate % 32 (MXFP4 rows, :1043); W4A4 also
+ * needs hidden and intermediate % 128.  The reference's tokens % 64 rule
+ * (:946) is lifted.  Scratch memory is owned by the context. */
+int mx_mlp_forward(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const void* x,
+                   const mx_mlp_weights* w, void* out);
+
+/* Timed loop as runMXFP4FusedMLPBenchmarkVariant (main.swift:1953-2031):
+ * `warmup` untimed iterations, then `iterations` back-to-back forwards on the
+ * stream between two HIP events.  Iteration i uses weight set i % n_sets
+ * (MoE-style rotation; defeats the 256 MB last-level cache).
+ * seconds_out: total timed seconds.  kernel_us_out (optional, length
+ * >= 8): average device time per iteration of each kernel of the forward, in
+ * launch order, from events around each launch in a second timed pass;
+ * n_kernels_out: how many were written. */
+int mx_mlp_benchmark(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const void* x,
+                     const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
+                     int iterations, double* seconds_out, double* kernel_us_out,
+                     int* n_kernels_out);
+/* Name of kernel `index` of a variant's forward (for the per-kernel times). */
+const char* mx_mlp_kernel_name(int variant, int tokens, int index);
+
+/* ---- weight-format rows (config 3) ------------------------------------------ */
+/* Quantize f32 weights [rows][k] into format `wfmt` (scales per the enum). */
+int mx_fmt_quantize(mx_ctx* ctx, int wfmt, const float* w, int rows, int k, void* q,
+                    void* scales);
+/* MLP with format weights: mpp_mlp_h_fp8e4m3_f_n128 / _h_fp8e5m2_f_n128 /
+ * h_i8_f / h_i4_f / i8_i8_i32 rows (MPPMLPKernels.metal:50-125) with scales. */
+int mx_fmt_mlp_forward(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,
+                       const mx_mlp_weights* w, void* out);
+int mx_fmt_mlp_benchmark(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,
+                         const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
+                         int iterations, double* seconds_out);
+
+/* ---- synthetic data (main.swift:2785-2842) ---------------------------------- */
+/* Seeded N(mean, std) on the device (f32 or f16). */
+int mx_fill_normal(mx_ctx* ctx, void* dst, int dtype, size_t n, uint64_t seed, float mean,
+                   float stddev);
+/* Reference LCG generators, bit-exact (host memory; no context needed):
+ * state = state*1664525 + 1013904223 + index, applied before each use. */
+void mx_lcg_bytes(uint32_t seed, size_t count, uint8_t* host_out);          /* makePackedMatrixBytes :2785 */
+void mx_lcg_pattern(uint32_t seed, size_t count, const uint8_t* pattern, int pattern_count,
+                    uint8_t* host_out);                                     /* makeBytePatternValues :2812 */
+void mx_lcg_half(uint32_t seed, size_t count, float scale, uint16_t* host_out); /* makeHalfMatrixValues :2822 */
+void mx_lcg_int8(uint32_t seed, size_t count, int8_t* host_out);            /* makeInt8MatrixValues :2834 */
+/* Checksums (sampleFloatChecksum / sampleIntChecksum / sampleHalfRawChecksum,
+ * main.swift:2844-2884): sum of every max(1, count/32)-th element. */
+double mx_checksum_f32(const float* host_p, size_t count, int* samples);
+int64_t mx_checksum_i32(const int32_t* host_p, size_t count, int* samples);
+uint64_t mx_checksum_f16raw(const uint16_t* host_p, size_t count, int* samples);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MXFP4HIP_H */

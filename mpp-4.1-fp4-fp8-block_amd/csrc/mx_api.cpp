@@ -1,0 +1,715 @@
+// mx_api.cpp - the C ABI of libmxfp4hip (declared in include/mxfp4hip.h).
+//
+// Owns the device, one HIP stream, scratch memory and every launch; checks
+// arguments the way runMLPBenchmark does (main.swift:592-597) and maps
+// failures onto the reference's ProbeError cases (main.swift:5-38).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "../../include/mxfp4hip.h"
+#include "mx_internal.h"
+
+struct mx_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  std::string err;
+  char name[256] = {0};
+  int cus = 0, clock_mhz = 0;
+  // scratch owned by the context (grown on demand; counters zeroed once)
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  uint32_t* counters = nullptr;  // two regions of kMaxCounters
+};
+
+namespace {
+
+constexpr size_t kMaxCounters = 1 << 16;  // row groups per GEMV phase
+
+int set_err(mx_ctx* c, int code, const char* fmt, ...) {
+  if (c) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    c->err = buf;
+  }
+  return code;
+}
+
+#define MX_HIP(ctx, expr)                                                                 \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess)                                                                 \
+      return set_err(ctx, MX_EGPU, "%s failed: %s", #expr, hipGetErrorString(e_));        \
+  } while (0)
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int ensure_ws(mx_ctx* c, size_t bytes) {
+  if (bytes <= c->ws_bytes) return MX_OK;
+  if (c->ws) {
+    MX_HIP(c, hipStreamSynchronize(c->stream));
+    MX_HIP(c, hipFree(c->ws));
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+  }
+  size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+  if (hipMalloc(&c->ws, want) != hipSuccess) {
+    c->ws = nullptr;
+    return set_err(c, MX_ENOMEM, "Could not create device buffer workspace (%zu bytes).", want);
+  }
+  c->ws_bytes = want;
+  return MX_OK;
+}
+
+int ensure_counters(mx_ctx* c) {
+  if (c->counters) return MX_OK;
+  if (hipMalloc(reinterpret_cast<void**>(&c->counters), 2 * kMaxCounters * sizeof(uint32_t)) !=
+      hipSuccess) {
+    c->counters = nullptr;
+    return set_err(c, MX_ENOMEM, "Could not create device buffer counters.");
+  }
+  MX_HIP(c, hipMemsetAsync(c->counters, 0, 2 * kMaxCounters * sizeof(uint32_t), c->stream));
+  MX_HIP(c, hipStreamSynchronize(c->stream));
+  return MX_OK;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// A forward pass as a list of launches (so the benchmark can time each).
+struct Step {
+  const char* name;
+  std::function<hipError_t()> run;
+};
+
+int check_mlp_cfg(mx_ctx* c, int variant, const mx_mlp_config* cfg) {
+  if (!cfg) return set_err(c, MX_EINVAL, "MLP config is null.");
+  const long T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
+  if (T <= 0 || H <= 0 || I <= 0)
+    return set_err(c, MX_EINVAL, "MLP sizes and iterations must be positive.");
+  if (H % 16 || I % 16)
+    return set_err(c, MX_EINVAL,
+                   "MLP hidden and intermediate sizes must be multiples of 16 for packed FP4 weights.");
+  if (H % 32 || I % 32)
+    return set_err(c, MX_EINVAL, "MXFP4 rows need hidden and intermediate to be multiples of 32.");
+  if (H % 64 || I % 64)
+    return set_err(c, MX_EINVAL, "hidden and intermediate must be multiples of 64 (MFMA tile).");
+  if (variant == MX_MLP_W4A4 && (H % 128 || I % 128))
+    return set_err(c, MX_EINVAL, "W4A4 needs hidden and intermediate to be multiples of 128.");
+  if (variant < MX_MLP_FUSED || variant > MX_MLP_REFROW)
+    return set_err(c, MX_EINVAL, "Unknown MLP variant %d.", variant);
+  return MX_OK;
+}
+
+bool gemv_ok(const mx_mlp_config* cfg) {
+  return cfg->tokens <= 16 && cfg->hidden % 128 == 0 && cfg->intermediate % 128 == 0 &&
+         cfg->hidden / 16 <= kMaxCounters && cfg->intermediate / 16 <= kMaxCounters;
+}
+
+// Scratch layout for one variant; returns bytes needed.
+struct MlpScratch {
+  size_t mid = 0, gate = 0, up = 0, wg = 0, wu = 0, wd = 0, xq = 0, xs = 0, mq = 0, ms = 0;
+  size_t part = 0, total = 0;
+};
+
+MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
+  const size_t T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
+  MlpScratch s;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
+  if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
+    s.mid = take(T * I * 2);
+    if (variant == MX_MLP_FUSED && gemv_ok(cfg)) {
+      const int sp_gu = mx::gemv_pick_splits((int)I, (int)H, 1);
+      const int sp_d = mx::gemv_pick_splits((int)H, (int)I, 0);
+      size_t p = mx::gemv_partial_floats((int)T, (int)I, sp_gu, 1);
+      size_t p2 = mx::gemv_partial_floats((int)T, (int)H, sp_d, 0);
+      s.part = take((p > p2 ? p : p2) * 4);
+    }
+  } else if (variant == MX_MLP_DEQUANT) {
+    s.wg = take(I * H * 2);
+    s.wu = take(I * H * 2);
+    s.wd = take(H * I * 2);
+    s.gate = take(T * I * 4);
+    s.up = take(T * I * 4);
+    s.mid = take(T * I * 4);
+  } else if (variant == MX_MLP_W4A4) {
+    s.xq = take(T * H / 2);
+    s.xs = take(T * H / 32);
+    s.mq = take(T * I / 2);
+    s.ms = take(T * I / 32);
+  }
+  s.total = off;
+  return s;
+}
+
+int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void* x,
+                    const mx_mlp_weights* w, void* out, std::vector<Step>& steps) {
+  int rc = check_mlp_cfg(c, variant, cfg);
+  if (rc) return rc;
+  if (!x || !w || !out) return set_err(c, MX_EINVAL, "MLP buffers must not be null.");
+  const mx_qmatrix* mats[3] = {&w->gate, &w->up, &w->down};
+  for (const mx_qmatrix* m : mats) {
+    if (!m->data || !m->scales) return set_err(c, MX_EINVAL, "MLP weight buffers must not be null.");
+    if (!aligned16(m->data)) return set_err(c, MX_EINVAL, "MXFP4 weight data must be 16-byte aligned.");
+    if (variant == MX_MLP_W4A4 && (reinterpret_cast<uintptr_t>(m->scales) & 3u))
+      return set_err(c, MX_EINVAL, "W4A4 scale planes must be 4-byte aligned.");
+  }
+  if (!aligned16(x) || !aligned16(out))
+    return set_err(c, MX_EINVAL, "Activation and output buffers must be 16-byte aligned.");
+  MlpScratch s = plan_scratch(variant, cfg);
+  if ((rc = ensure_ws(c, s.total))) return rc;
+  if ((rc = ensure_counters(c))) return rc;
+  uint8_t* ws = static_cast<uint8_t*>(c->ws);
+  hipStream_t st = c->stream;
+  const int T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
+  const uint8_t* wg = static_cast<const uint8_t*>(w->gate.data);
+  const uint8_t* sg = static_cast<const uint8_t*>(w->gate.scales);
+  const uint8_t* wu = static_cast<const uint8_t*>(w->up.data);
+  const uint8_t* su = static_cast<const uint8_t*>(w->up.scales);
+  const uint8_t* wd = static_cast<const uint8_t*>(w->down.data);
+  const uint8_t* sd = static_cast<const uint8_t*>(w->down.scales);
+
+  if (variant == MX_MLP_FUSED && gemv_ok(cfg)) {
+    uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
+    float* part = reinterpret_cast<float*>(ws + s.part);
+    mx::GemvArgs gu{static_cast<const uint16_t*>(x), wg, sg, wu, su, mid, part, c->counters,
+                    T, I, H, mx::gemv_pick_splits(I, H, 1)};
+    mx::GemvArgs dn{mid, wd, sd, nullptr, nullptr, static_cast<uint16_t*>(out), part,
+                    c->counters + kMaxCounters, T, H, I, mx::gemv_pick_splits(H, I, 0)};
+    steps.push_back({"gemv_mxfp4_gate_up_swiglu", [=] { return mx::launch_gemv_mxfp4(1, gu, st); }});
+    steps.push_back({"gemv_mxfp4_down", [=] { return mx::launch_gemv_mxfp4(0, dn, st); }});
+  } else if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
+    uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
+    const bool ref = variant == MX_MLP_REFROW;
+    mx::GemmArgs gu{x, MX_DTYPE_F16, wg, sg, wu, su, mid, T, I, H};
+    mx::GemmArgs dn{mid, MX_DTYPE_F16, wd, sd, nullptr, nullptr, out, T, H, I};
+    steps.push_back({ref ? "gemm_h_mxfp4_gate_up_swiglu_half" : "gemm_h_mxfp4_gate_up_swiglu",
+                     [=] { return mx::launch_gemm_h(mx::BK_MXFP4, ref ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16, gu, st); }});
+    steps.push_back({ref ? "gemm_h_mxfp4_down_f32" : "gemm_h_mxfp4_down",
+                     [=] { return mx::launch_gemm_h(mx::BK_MXFP4, ref ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16, dn, st); }});
+  } else if (variant == MX_MLP_DEQUANT) {
+    uint16_t* wg16 = reinterpret_cast<uint16_t*>(ws + s.wg);
+    uint16_t* wu16 = reinterpret_cast<uint16_t*>(ws + s.wu);
+    uint16_t* wd16 = reinterpret_cast<uint16_t*>(ws + s.wd);
+    float* gate = reinterpret_cast<float*>(ws + s.gate);
+    float* up = reinterpret_cast<float*>(ws + s.up);
+    float* mid = reinterpret_cast<float*>(ws + s.mid);
+    steps.push_back({"dequant_gate", [=] { return mx::launch_mxfp4_dequant_f16(wg, sg, wg16, I, H, st); }});
+    steps.push_back({"dequant_up", [=] { return mx::launch_mxfp4_dequant_f16(wu, su, wu16, I, H, st); }});
+    steps.push_back({"dequant_down", [=] { return mx::launch_mxfp4_dequant_f16(wd, sd, wd16, H, I, st); }});
+    mx::GemmArgs gg{x, MX_DTYPE_F16, wg16, nullptr, nullptr, nullptr, gate, T, I, H};
+    mx::GemmArgs gp{x, MX_DTYPE_F16, wu16, nullptr, nullptr, nullptr, up, T, I, H};
+    mx::GemmArgs dn{mid, MX_DTYPE_F32, wd16, nullptr, nullptr, nullptr, out, T, H, I};
+    steps.push_back({"gemm_h_h_f_gate", [=] { return mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F32, gg, st); }});
+    steps.push_back({"gemm_h_h_f_up", [=] { return mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F32, gp, st); }});
+    steps.push_back({"swiglu_float", [=] { return mx::launch_swiglu(0, gate, up, mid, (size_t)T * I, st); }});
+    steps.push_back({"gemm_f_h_down", [=] { return mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F16, dn, st); }});
+  } else {  // W4A4
+    uint8_t* xq = ws + s.xq;
+    uint8_t* xs = ws + s.xs;
+    uint8_t* mq = ws + s.mq;
+    uint8_t* ms = ws + s.ms;
+    mx::Fp4GemmArgs gu{xq, xs, wg, sg, wu, su, mq, ms, T, I, H};
+    mx::Fp4GemmArgs dn{mq, ms, wd, sd, nullptr, nullptr, out, nullptr, T, H, I};
+    steps.push_back({"quantize_x_mxfp4", [=] { return mx::launch_mxfp4_quantize(x, MX_DTYPE_F16, xq, xs, T, H, st); }});
+    steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
+    steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});
+  }
+  return MX_OK;
+}
+
+int run_steps(mx_ctx* c, const std::vector<Step>& steps) {
+  for (const Step& s : steps) {
+    hipError_t e = s.run();
+    if (e != hipSuccess) return set_err(c, MX_EGPU, "launch of %s failed: %s", s.name, hipGetErrorString(e));
+  }
+  return MX_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+const char* mx_status_string(int status) {
+  switch (status) {
+    case MX_OK: return "ok";
+    case MX_EINVAL: return "invalid argument";
+    case MX_ENODEV: return "No HIP device is available.";
+    case MX_ENOKERNEL: return "The HIP code object does not contain the kernel for this device.";
+    case MX_ENOMEM: return "Could not create device buffer.";
+    case MX_EGPU: return "GPU execution failed.";
+  }
+  return "unknown status";
+}
+
+int mx_create(int device, mx_ctx** out) {
+  if (!out) return MX_EINVAL;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return MX_ENODEV;
+  if (device < 0 || device >= n) return MX_ENODEV;
+  mx_ctx* c = new mx_ctx();
+  c->device = device;
+  if (hipSetDevice(device) != hipSuccess) { delete c; return MX_ENODEV; }
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, device) != hipSuccess) { delete c; return MX_ENODEV; }
+  if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) { delete c; return MX_ENOKERNEL; }
+  std::snprintf(c->name, sizeof c->name, "%s (%s)", p.name, p.gcnArchName);
+  c->cus = p.multiProcessorCount;
+  c->clock_mhz = p.clockRate / 1000;
+  if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return MX_EGPU;
+  }
+  c->stream = c->own_stream;
+  *out = c;
+  return MX_OK;
+}
+
+void mx_destroy(mx_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->ws) (void)hipFree(c->ws);
+  if (c->counters) (void)hipFree(c->counters);
+  if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+  delete c;
+}
+
+const char* mx_last_error(const mx_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+int mx_device_info(mx_ctx* c, char* name_out, size_t name_len, int* cu_count, int* clock_mhz) {
+  if (!c) return MX_EINVAL;
+  if (name_out && name_len) std::snprintf(name_out, name_len, "%s", c->name);
+  if (cu_count) *cu_count = c->cus;
+  if (clock_mhz) *clock_mhz = c->clock_mhz;
+  return MX_OK;
+}
+
+int mx_set_stream(mx_ctx* c, void* stream) {
+  if (!c) return MX_EINVAL;
+  c->stream = stream ? static_cast<hipStream_t>(stream) : c->own_stream;
+  return MX_OK;
+}
+
+void* mx_get_stream(mx_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+
+int mx_sync(mx_ctx* c) {
+  if (!c) return MX_EINVAL;
+  MX_HIP(c, hipStreamSynchronize(c->stream));
+  return MX_OK;
+}
+
+int mx_alloc(mx_ctx* c, size_t bytes, void** dptr) {
+  if (!c || !dptr) return MX_EINVAL;
+  *dptr = nullptr;
+  if (bytes == 0) return set_err(c, MX_EINVAL, "allocation size must be positive.");
+  if (hipMalloc(dptr, bytes) != hipSuccess) {
+    *dptr = nullptr;
+    (void)hipGetLastError();
+    return set_err(c, MX_ENOMEM, "Could not create device buffer of %zu bytes.", bytes);
+  }
+  return MX_OK;
+}
+
+int mx_free(mx_ctx* c, void* dptr) {
+  if (!c) return MX_EINVAL;
+  if (dptr) MX_HIP(c, hipFree(dptr));
+  return MX_OK;
+}
+
+int mx_upload(mx_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return MX_EINVAL;
+  MX_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  MX_HIP(c, hipStreamSynchronize(c->stream));
+  return MX_OK;
+}
+
+int mx_download(mx_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return MX_EINVAL;
+  MX_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  MX_HIP(c, hipStreamSynchronize(c->stream));
+  return MX_OK;
+}
+
+int mx_memset(mx_ctx* c, void* dst, int value, size_t bytes) {
+  if (!c || (!dst && bytes)) return MX_EINVAL;
+  MX_HIP(c, hipMemsetAsync(dst, value, bytes, c->stream));
+  return MX_OK;
+}
+
+// ---- codecs ------------------------------------------------------------------
+static int check_fmt(mx_ctx* c, int fmt) {
+  if (fmt < MX_FMT_FP4_E2M1 || fmt > MX_FMT_FP8_E5M2)
+    return set_err(c, MX_EINVAL, "Unknown packed numeric format %d.", fmt);
+  return MX_OK;
+}
+
+int mx_pack(mx_ctx* c, int fmt, const float* in, size_t n, uint8_t* packed) {
+  if (!c) return MX_EINVAL;
+  if (int rc = check_fmt(c, fmt)) return rc;
+  if (n == 0) return MX_OK;
+  if (!in || !packed || !aligned16(in) || (reinterpret_cast<uintptr_t>(packed) & 3u))
+    return set_err(c, MX_EINVAL, "pack buffers must be non-null, input 16-byte and output 4-byte aligned.");
+  MX_HIP(c, mx::launch_pack(fmt, in, packed, n, c->stream));
+  return MX_OK;
+}
+
+int mx_unpack(mx_ctx* c, int fmt, const uint8_t* packed, size_t n, float* out) {
+  if (!c) return MX_EINVAL;
+  if (int rc = check_fmt(c, fmt)) return rc;
+  if (n == 0) return MX_OK;
+  if (!packed || !out || !aligned16(out) || (reinterpret_cast<uintptr_t>(packed) & 3u))
+    return set_err(c, MX_EINVAL, "unpack buffers must be non-null, output 16-byte and input 4-byte aligned.");
+  MX_HIP(c, mx::launch_unpack(fmt, packed, out, n, c->stream));
+  return MX_OK;
+}
+
+int mx_roundtrip(mx_ctx* c, int fmt, const float* host_in, size_t n, uint8_t* host_packed,
+                 float* host_out) {
+  if (!c) return MX_EINVAL;
+  if (int rc = check_fmt(c, fmt)) return rc;
+  if (n == 0) return MX_OK;
+  if (!host_in || !host_packed || !host_out)
+    return set_err(c, MX_EINVAL, "roundtrip buffers must not be null.");
+  const size_t pbytes = fmt == MX_FMT_FP4_E2M1 ? (n + 1) / 2 : n;
+  void *din = nullptr, *dp = nullptr, *dout = nullptr;
+  int rc = MX_OK;
+  if ((rc = mx_alloc(c, n * 4, &din)) || (rc = mx_alloc(c, align_up(pbytes, 16), &dp)) ||
+      (rc = mx_alloc(c, n * 4, &dout))) {
+    mx_free(c, din); mx_free(c, dp); mx_free(c, dout);
+    return rc;
+  }
+  do {
+    if ((rc = mx_upload(c, din, host_in, n * 4))) break;
+    if ((rc = mx_memset(c, dp, 0, align_up(pbytes, 16)))) break;
+    if ((rc = mx_pack(c, fmt, static_cast<float*>(din), n, static_cast<uint8_t*>(dp)))) break;
+    if ((rc = mx_unpack(c, fmt, static_cast<uint8_t*>(dp), n, static_cast<float*>(dout)))) break;
+    if ((rc = mx_download(c, host_packed, dp, pbytes))) break;
+    if ((rc = mx_download(c, host_out, dout, n * 4))) break;
+  } while (0);
+  mx_free(c, din); mx_free(c, dp); mx_free(c, dout);
+  return rc;
+}
+
+int mx_mxfp4_quantize(mx_ctx* c, const void* src, int src_dtype, int rows, int k, uint8_t* packed,
+                      uint8_t* scales) {
+  if (!c) return MX_EINVAL;
+  if (rows <= 0 || k <= 0 || k % 32)
+    return set_err(c, MX_EINVAL, "quantize needs rows > 0 and k a positive multiple of 32.");
+  if (src_dtype != MX_DTYPE_F16 && src_dtype != MX_DTYPE_F32)
+    return set_err(c, MX_EINVAL, "quantize source must be f16 or f32.");
+  if (!src || !packed || !scales || !aligned16(src) || !aligned16(packed))
+    return set_err(c, MX_EINVAL, "quantize buffers must be non-null and 16-byte aligned.");
+  MX_HIP(c, mx::launch_mxfp4_quantize(src, src_dtype, packed, scales, rows, k, c->stream));
+  return MX_OK;
+}
+
+int mx_mxfp4_dequant_f16(mx_ctx* c, const uint8_t* packed, const uint8_t* scales, void* out, int rows,
+                         int depth) {
+  if (!c) return MX_EINVAL;
+  if (rows <= 0 || depth <= 0 || depth % 32)
+    return set_err(c, MX_EINVAL, "dequant needs rows > 0 and depth a positive multiple of 32.");
+  if (!packed || !scales || !out || !aligned16(packed) || !aligned16(out))
+    return set_err(c, MX_EINVAL, "dequant buffers must be non-null and 16-byte aligned.");
+  MX_HIP(c, mx::launch_mxfp4_dequant_f16(packed, scales, static_cast<uint16_t*>(out), rows, depth, c->stream));
+  return MX_OK;
+}
+
+static int check_gemm(mx_ctx* c, int m, int n, int k, const void* a, const void* b, const void* out) {
+  if (m <= 0 || n <= 0 || k <= 0) return set_err(c, MX_EINVAL, "matmul sizes must be positive.");
+  if (n % 64) return set_err(c, MX_EINVAL, "matmul n must be a multiple of 64.");
+  if (k % 32) return set_err(c, MX_EINVAL, "matmul k must be a multiple of 32.");
+  if (!a || !b || !out || !aligned16(a) || !aligned16(b) || !aligned16(out))
+    return set_err(c, MX_EINVAL, "matmul buffers must be non-null and 16-byte aligned.");
+  return MX_OK;
+}
+
+int mx_mxfp4_matmul(mx_ctx* c, const void* a, int a_dtype, const uint8_t* b, void* out, int c_dtype,
+                    int m, int n, int k, const uint8_t* scales) {
+  if (!c) return MX_EINVAL;
+  if (int rc = check_gemm(c, m, n, k, a, b, out)) return rc;
+  if (!scales) return set_err(c, MX_EINVAL, "matmul scales must not be null.");
+  if (a_dtype != MX_DTYPE_F16 && a_dtype != MX_DTYPE_F32)
+    return set_err(c, MX_EINVAL, "matmul A must be f16 or f32.");
+  if (c_dtype != MX_DTYPE_F32 && c_dtype != MX_DTYPE_F16)
+    return set_err(c, MX_EINVAL, "matmul C must be f32 or f16.");
+  mx::GemmArgs g{a, a_dtype, b, scales, nullptr, nullptr, out, m, n, k};
+  MX_HIP(c, mx::launch_gemm_h(mx::BK_MXFP4, c_dtype == MX_DTYPE_F32 ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16,
+                              g, c->stream));
+  return MX_OK;
+}
+
+int mx_gemm_f16(mx_ctx* c, const void* a, int a_dtype, const void* b, float* out, int m, int n, int k) {
+  if (!c) return MX_EINVAL;
+  if (int rc = check_gemm(c, m, n, k, a, b, out)) return rc;
+  if (a_dtype != MX_DTYPE_F16 && a_dtype != MX_DTYPE_F32)
+    return set_err(c, MX_EINVAL, "gemm A must be f16 or f32.");
+  mx::GemmArgs g{a, a_dtype, b, nullptr, nullptr, nullptr, out, m, n, k};
+  MX_HIP(c, mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F32, g, c->stream));
+  return MX_OK;
+}
+
+int mx_swiglu(mx_ctx* c, int variant, const void* gate, const void* up, void* mid, int tokens,
+              int intermediate) {
+  if (!c) return MX_EINVAL;
+  if (variant < 0 || variant > 3) return set_err(c, MX_EINVAL, "Unknown SwiGLU variant %d.", variant);
+  if (tokens <= 0 || intermediate <= 0) return set_err(c, MX_EINVAL, "SwiGLU sizes must be positive.");
+  if (!gate || !up || !mid) return set_err(c, MX_EINVAL, "SwiGLU buffers must not be null.");
+  MX_HIP(c, mx::launch_swiglu(variant, gate, up, mid, (size_t)tokens * intermediate, c->stream));
+  return MX_OK;
+}
+
+// ---- MLP ------------------------------------------------------------------------
+int mx_mlp_forward(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void* x,
+                   const mx_mlp_weights* w, void* out) {
+  if (!c) return MX_EINVAL;
+  std::vector<Step> steps;
+  if (int rc = build_mlp_steps(c, variant, cfg, x, w, out, steps)) return rc;
+  return run_steps(c, steps);
+}
+
+const char* mx_mlp_kernel_name(int variant, int tokens, int index) {
+  static const char* fused_gemv[] = {"gemv_mxfp4_gate_up_swiglu", "gemv_mxfp4_down"};
+  static const char* fused[] = {"gemm_h_mxfp4_gate_up_swiglu", "gemm_h_mxfp4_down"};
+  static const char* ref[] = {"gemm_h_mxfp4_gate_up_swiglu_half", "gemm_h_mxfp4_down_f32"};
+  static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
+                              "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
+  static const char* w4[] = {"quantize_x_mxfp4", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down"};
+  if (index < 0) return nullptr;
+  switch (variant) {
+    case MX_MLP_FUSED: return index < 2 ? (tokens <= 16 ? fused_gemv[index] : fused[index]) : nullptr;
+    case MX_MLP_REFROW: return index < 2 ? ref[index] : nullptr;
+    case MX_MLP_DEQUANT: return index < 7 ? deq[index] : nullptr;
+    case MX_MLP_W4A4: return index < 3 ? w4[index] : nullptr;
+  }
+  return nullptr;
+}
+
+static int bench_loop(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int warmup,
+                      int iterations, double* seconds_out, double* kernel_us_out,
+                      int* n_kernels_out) {
+  if (iterations <= 0 || warmup < 0)
+    return set_err(c, MX_EINVAL, "MLP sizes and iterations must be positive.");
+  const int ns = (int)sets.size();
+  for (int i = 0; i < warmup; i++)
+    if (int rc = run_steps(c, sets[i % ns])) return rc;
+  hipEvent_t e0, e1;
+  MX_HIP(c, hipEventCreate(&e0));
+  MX_HIP(c, hipEventCreate(&e1));
+  int rc = MX_OK;
+  do {
+    if (hipStreamSynchronize(c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "sync failed"); break; }
+    if (hipEventRecord(e0, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
+    for (int i = 0; i < iterations && !rc; i++) rc = run_steps(c, sets[i % ns]);
+    if (rc) break;
+    if (hipEventRecord(e1, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
+    if (hipEventSynchronize(e1) != hipSuccess) { rc = set_err(c, MX_EGPU, "MXFP4 MLP timed loop failed."); break; }
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    if (seconds_out) *seconds_out = ms / 1000.0;
+  } while (0);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  if (kernel_us_out || n_kernels_out) {
+    // Second pass: an event before and after every launch.
+    const int nk = (int)sets[0].size();
+    if (n_kernels_out) *n_kernels_out = nk > 8 ? 8 : nk;
+    std::vector<hipEvent_t> ev((size_t)iterations * (nk + 1));
+    for (auto& e : ev) MX_HIP(c, hipEventCreate(&e));
+    for (int i = 0; i < iterations && !rc; i++) {
+      const auto& steps = sets[i % ns];
+      (void)hipEventRecord(ev[(size_t)i * (nk + 1)], c->stream);
+      for (int k = 0; k < nk && !rc; k++) {
+        hipError_t e = steps[k].run();
+        if (e != hipSuccess) rc = set_err(c, MX_EGPU, "launch of %s failed: %s", steps[k].name, hipGetErrorString(e));
+        (void)hipEventRecord(ev[(size_t)i * (nk + 1) + k + 1], c->stream);
+      }
+    }
+    if (!rc && hipStreamSynchronize(c->stream) != hipSuccess) rc = set_err(c, MX_EGPU, "sync failed");
+    if (!rc && kernel_us_out) {
+      for (int k = 0; k < nk && k < 8; k++) {
+        double tot = 0.0;
+        for (int i = 0; i < iterations; i++) {
+          float ms = 0.0f;
+          (void)hipEventElapsedTime(&ms, ev[(size_t)i * (nk + 1) + k], ev[(size_t)i * (nk + 1) + k + 1]);
+          tot += ms;
+        }
+        kernel_us_out[k] = tot * 1000.0 / iterations;
+      }
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+  }
+  return rc;
+}
+
+int mx_mlp_benchmark(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void* x,
+                     const mx_mlp_weights* sets, int n_sets, void* out, int warmup, int iterations,
+                     double* seconds_out, double* kernel_us_out, int* n_kernels_out) {
+  if (!c) return MX_EINVAL;
+  if (!sets || n_sets <= 0) return set_err(c, MX_EINVAL, "benchmark needs at least one weight set.");
+  std::vector<std::vector<Step>> all((size_t)n_sets);
+  for (int i = 0; i < n_sets; i++)
+    if (int rc = build_mlp_steps(c, variant, cfg, x, &sets[i], out, all[i])) return rc;
+  return bench_loop(c, all, warmup, iterations, seconds_out, kernel_us_out, n_kernels_out);
+}
+
+// ---- weight formats ---------------------------------------------------------------
+int mx_fmt_quantize(mx_ctx* c, int wfmt, const float* w, int rows, int k, void* q, void* scales) {
+  if (!c) return MX_EINVAL;
+  if (rows <= 0 || k <= 0 || k % 32) return set_err(c, MX_EINVAL, "format quantize needs k % 32 == 0.");
+  if (!w || !q || !scales || !aligned16(w) || !aligned16(q))
+    return set_err(c, MX_EINVAL, "format quantize buffers must be non-null and 16-byte aligned.");
+  switch (wfmt) {
+    case MX_WFMT_FP8_E4M3:
+    case MX_WFMT_FP8_E5M2:
+    case MX_WFMT_INT8:
+    case MX_WFMT_W8A8:
+      MX_HIP(c, mx::launch_quant_rowwise(wfmt == MX_WFMT_W8A8 ? MX_WFMT_INT8 : wfmt, w, rows, k,
+                                         static_cast<uint8_t*>(q), static_cast<float*>(scales), c->stream));
+      return MX_OK;
+    case MX_WFMT_INT4:
+      MX_HIP(c, mx::launch_quant_int4_g32(w, rows, k, static_cast<uint8_t*>(q),
+                                          static_cast<uint16_t*>(scales), c->stream));
+      return MX_OK;
+  }
+  return set_err(c, MX_EINVAL, "Unknown weight format %d.", wfmt);
+}
+
+static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const void* x,
+                           const mx_mlp_weights* w, void* out, std::vector<Step>& steps) {
+  if (int rc = check_mlp_cfg(c, MX_MLP_FUSED, cfg)) return rc;
+  if (!x || !w || !out) return set_err(c, MX_EINVAL, "MLP buffers must not be null.");
+  int bk;
+  switch (wfmt) {
+    case MX_WFMT_FP8_E4M3: bk = mx::BK_E4M3; break;
+    case MX_WFMT_FP8_E5M2: bk = mx::BK_E5M2; break;
+    case MX_WFMT_INT8: bk = mx::BK_INT8; break;
+    case MX_WFMT_INT4: bk = mx::BK_INT4G32; break;
+    case MX_WFMT_W8A8: return set_err(c, MX_EINVAL, "W8A8 MLP is not available in this build.");
+    default: return set_err(c, MX_EINVAL, "Unknown weight format %d.", wfmt);
+  }
+  const mx_qmatrix* mats[3] = {&w->gate, &w->up, &w->down};
+  for (const mx_qmatrix* m : mats)
+    if (!m->data || !m->scales || !aligned16(m->data))
+      return set_err(c, MX_EINVAL, "format weight buffers must be non-null and 16-byte aligned.");
+  const int T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
+  if (int rc = ensure_ws(c, align_up((size_t)T * I * 2, 256))) return rc;
+  uint16_t* mid = static_cast<uint16_t*>(c->ws);
+  hipStream_t st = c->stream;
+  mx::GemmArgs gu{x, MX_DTYPE_F16, w->gate.data, w->gate.scales, w->up.data, w->up.scales, mid, T, I, H};
+  mx::GemmArgs dn{mid, MX_DTYPE_F16, w->down.data, w->down.scales, nullptr, nullptr, out, T, H, I};
+  steps.push_back({"gemm_h_fmt_gate_up_swiglu", [=] { return mx::launch_gemm_h(bk, mx::EPI_SWIGLU_F16, gu, st); }});
+  steps.push_back({"gemm_h_fmt_down", [=] { return mx::launch_gemm_h(bk, mx::EPI_STORE_F16, dn, st); }});
+  return MX_OK;
+}
+
+int mx_fmt_mlp_forward(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const void* x,
+                       const mx_mlp_weights* w, void* out) {
+  if (!c) return MX_EINVAL;
+  std::vector<Step> steps;
+  if (int rc = build_fmt_steps(c, wfmt, cfg, x, w, out, steps)) return rc;
+  return run_steps(c, steps);
+}
+
+int mx_fmt_mlp_benchmark(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const void* x,
+                         const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
+                         int iterations, double* seconds_out) {
+  if (!c) return MX_EINVAL;
+  if (!sets || n_sets <= 0) return set_err(c, MX_EINVAL, "benchmark needs at least one weight set.");
+  std::vector<std::vector<Step>> all((size_t)n_sets);
+  for (int i = 0; i < n_sets; i++)
+    if (int rc = build_fmt_steps(c, wfmt, cfg, x, &sets[i], out, all[i])) return rc;
+  return bench_loop(c, all, warmup, iterations, seconds_out, nullptr, nullptr);
+}
+
+// ---- synthetic data ------------------------------------------------------------------
+int mx_fill_normal(mx_ctx* c, void* dst, int dtype, size_t n, uint64_t seed, float mean, float stddev) {
+  if (!c) return MX_EINVAL;
+  if (dtype != MX_DTYPE_F32 && dtype != MX_DTYPE_F16)
+    return set_err(c, MX_EINVAL, "fill_normal dtype must be f32 or f16.");
+  if (n && !dst) return set_err(c, MX_EINVAL, "fill_normal buffer must not be null.");
+  MX_HIP(c, mx::launch_fill_normal(dst, dtype, n, seed, mean, stddev, c->stream));
+  return MX_OK;
+}
+
+static inline uint16_t host_f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;  // host compiler: IEEE RNE
+  uint16_t u;
+  std::memcpy(&u, &h, 2);
+  return u;
+}
+
+void mx_lcg_bytes(uint32_t seed, size_t count, uint8_t* out) {
+  uint32_t s = seed;
+  for (size_t i = 0; i < count; i++) {
+    s = s * 1664525u + 1013904223u + (uint32_t)i;
+    out[i] = (uint8_t)(s >> 16);
+  }
+}
+
+void mx_lcg_pattern(uint32_t seed, size_t count, const uint8_t* pattern, int pattern_count, uint8_t* out) {
+  uint32_t s = seed;
+  for (size_t i = 0; i < count; i++) {
+    s = s * 1664525u + 1013904223u + (uint32_t)i;
+    out[i] = pattern[s % (uint32_t)pattern_count];
+  }
+}
+
+void mx_lcg_half(uint32_t seed, size_t count, float scale, uint16_t* out) {
+  uint32_t s = seed;
+  for (size_t i = 0; i < count; i++) {
+    s = s * 1664525u + 1013904223u + (uint32_t)i;
+    const int nib = (int)((s >> 28) & 15u);
+    out[i] = host_f32_to_f16((float)((nib ^ 8) - 8) * scale);
+  }
+}
+
+void mx_lcg_int8(uint32_t seed, size_t count, int8_t* out) {
+  uint32_t s = seed;
+  for (size_t i = 0; i < count; i++) {
+    s = s * 1664525u + 1013904223u + (uint32_t)i;
+    const int nib = (int)((s >> 28) & 15u);
+    out[i] = (int8_t)((nib ^ 8) - 8);
+  }
+}
+
+double mx_checksum_f32(const float* p, size_t count, int* samples) {
+  const size_t step = count / 32 > 1 ? count / 32 : 1;
+  double sum = 0.0;
+  int n = 0;
+  for (size_t i = 0; i < count; i += step) { sum += (double)p[i]; n++; }
+  if (samples) *samples = n;
+  return sum;
+}
+
+int64_t mx_checksum_i32(const int32_t* p, size_t count, int* samples) {
+  const size_t step = count / 32 > 1 ? count / 32 : 1;
+  int64_t sum = 0;
+  int n = 0;
+  for (size_t i = 0; i < count; i += step) { sum += p[i]; n++; }
+  if (samples) *samples = n;
+  return sum;
+}
+
+uint64_t mx_checksum_f16raw(const uint16_t* p, size_t count, int* samples) {
+  const size_t step = count / 32 > 1 ? count / 32 : 1;
+  uint64_t sum = 0;
+  int n = 0;
+  for (size_t i = 0; i < count; i += step) { sum += p[i]; n++; }
+  if (samples) *samples = n;
+  return sum;
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+// mx_device.h - gfx950 device helpers shared by the libmxfp4hip kernels.
+//
+// MXFP4 layout (reference GUIDE:43-55, MXFP4Kernels.metal:3-4, 98, 345):
+//   data   [N][K/2] bytes, two E2M1 codes per byte, low nibble = even k
+//   scales [N][K/32] E8M0 bytes, value 2^(byte-127)
+//
+// MFMA operand layouts used below (checked on gfx950 by the lane-layout
+// tests in tests/test_gpu_mfma_layout.py):
+//   v_mfma_scale_f32_32x32x64_f8f6f4 (fp4): lane l holds row l%32,
+//       k = 32*(l/32) + j, j = nibble j of 4 dwords (low nibble first);
+//       the lane's scale byte applies to exactly that (row, 32-k block).
+//   v_mfma_f32_32x32x16_f16: lane l holds row l%32, k = 8*(l/32) + j.
+//   v_mfma_f32_16x16x32_f16: lane l holds row l%16, k = 8*(l/16) + j.
+//   v_mfma_i32_32x32x32_i8:  lane l holds row l%32, k = 16*(l/32) + j.
+//   32x32 accumulators: lane l, reg v -> row (v/4)*8 + (l/32)*4 + v%4,
+//       column l%32.   16x16: row (l/16)*4 + v, column l%16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef short v2s __attribute__((ext_vector_type(2)));
+
+constexpr int kBlock = 32;  // MXFP4 block along K (MXFP4Kernels.metal:24)
+
+// E8M0 byte -> f32 with the reference's semantics: bits << 23
+// (MXFP4Kernels.metal:26-29): byte 0 -> 0.0, byte 255 -> +inf.
+__device__ __forceinline__ float e8m0_to_float(uint32_t b) {
+  return __builtin_bit_cast(float, b << 23);
+}
+
+// Scale operand for the gfx950 cvt_scalef32 instructions: the E8M0 byte in
+// the exponent field of an f32 (the hardware reads only that field).
+__device__ __forceinline__ float e8m0_as_cvt_scale(uint32_t b) {
+  return __builtin_bit_cast(float, (b & 255u) << 23);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32: RNE
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Two FP4 codes (byte `sel` of `src`) -> two halves, each fp4 * 2^(scale-127).
+template <int SEL>
+__device__ __forceinline__ v2h cvt_fp4x2_f16(uint32_t src, float scale) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(src, scale, SEL);
+}
+
+// 8 FP4 codes in a dword -> 8 halves (one 32x32x16 / 16x16x32 f16 operand).
+__device__ __forceinline__ v8h fp4x8_to_f16x8(uint32_t src, float scale) {
+  v2h a = cvt_fp4x2_f16<0>(src, scale);
+  v2h b = cvt_fp4x2_f16<1>(src, scale);
+  v2h c = cvt_fp4x2_f16<2>(src, scale);
+  v2h d = cvt_fp4x2_f16<3>(src, scale);
+  v8h r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+  return r;
+}
+
+// Dequantize 8 FP4 codes with E8M0 byte `sb` using the reference's scale
+// semantics (bits << 23).  Bytes 0..254 take the single-instruction path
+// (the hardware reads byte 0 as 2^-127, which gives the same halves as the
+// reference's 0.0 because 6 * 2^-127 underflows f16).  Byte 255 is +inf in
+// the reference but NaN to the hardware, so it takes an exact slow path.
+__device__ __forceinline__ v8h fp4x8_dequant_f16(uint32_t src, uint32_t sb) {
+  if (__builtin_expect(sb != 255u, 1)) return fp4x8_to_f16x8(src, e8m0_as_cvt_scale(sb));
+  const float inf = e8m0_to_float(255u);
+  v2f f[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 0),
+              __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 1),
+              __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 2),
+              __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 3)};
+  v8h h;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    h[2 * t] = (_Float16)(f[t][0] * inf);
+    h[2 * t + 1] = (_Float16)(f[t][1] * inf);
+  }
+  return h;
+}
+
+// Block amax -> E8M0 scale byte (BASELINE quantizer:
+// 2^(floor(log2(amax)) - 2)).  `amax_bits` = max of |x| bit patterns.
+// Non-finite -> 255, zero -> 127, exponents below -127 clamp to byte 0.
+__device__ __forceinline__ uint32_t mxfp4_scale_byte(uint32_t amax_bits) {
+  if (amax_bits >= 0x7f800000u) return 255u;
+  if (amax_bits == 0u) return 127u;
+  int fl;
+  uint32_t e = amax_bits >> 23;
+  if (e == 0) fl = (31 - __builtin_clz(amax_bits)) - 149;
+  else fl = (int)e - 127;
+  int s = fl - 2;
+  if (s < -127) s = -127;
+  return (uint32_t)(s + 127);
+}
+
+// Quantize 8 consecutive f32 values into one dword of 8 FP4 codes with the
+// block scale byte `sb` (0..254): code = RNE(x / 2^(sb-127)), saturating.
+__device__ __forceinline__ uint32_t fp4x8_from_f32(const float* v, uint32_t sb) {
+  float sc = e8m0_as_cvt_scale(sb);
+  uint32_t r = 0;
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, v[0], v[1], sc, 0);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, v[2], v[3], sc, 1);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, v[4], v[5], sc, 2);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, v[6], v[7], sc, 3);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t abs_bits(float f) {
+  return __builtin_bit_cast(uint32_t, f) & 0x7fffffffu;
+}
+
+// Accumulator element (lane, reg v) -> (row, col) within a 32x32 tile.
+__device__ __forceinline__ int acc32_row(int lane, int v) {
+  return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+}
+
+__device__ __forceinline__ v16f mfma_f16_32x32x16(v8h a, v8h b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4f mfma_f16_16x16x32(v8h a, v8h b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// FP4 x FP4 scaled MFMA.  OPSA/OPSB select the byte of the scale dwords.
+template <int OPSA, int OPSB>
+__device__ __forceinline__ v16f mfma_fp4_32x32x64(v4i a, v4i b, v16f c, int sa, int sb) {
+  v8i a8, b8;
+  a8[0] = a[0]; a8[1] = a[1]; a8[2] = a[2]; a8[3] = a[3];
+  a8[4] = 0; a8[5] = 0; a8[6] = 0; a8[7] = 0;
+  b8[0] = b[0]; b8[1] = b[1]; b8[2] = b[2]; b8[3] = b[3];
+  b8[4] = 0; b8[5] = 0; b8[6] = 0; b8[7] = 0;
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 4, 4, OPSA, sa, OPSB, sb);
+}
+
+}  // namespace mx

@@ -1,0 +1,85 @@
+// mx_internal.h - launcher declarations shared between the kernel files and
+// the C-ABI layer (mx_api.cpp).  Host-only types; no torch anywhere.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/mxfp4hip.h"
+
+namespace mx {
+
+// ---- codecs / elementwise (mx_codecs.hip) --------------------------------
+hipError_t launch_pack(int fmt, const float* in, uint8_t* out, size_t n, hipStream_t st);
+hipError_t launch_unpack(int fmt, const uint8_t* in, float* out, size_t n, hipStream_t st);
+hipError_t launch_mxfp4_quantize(const void* src, int src_dtype, uint8_t* packed, uint8_t* scales,
+                                 size_t rows, size_t k, hipStream_t st);
+hipError_t launch_mxfp4_dequant_f16(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
+                                    size_t rows, size_t depth, hipStream_t st);
+hipError_t launch_swiglu(int variant, const void* gate, const void* up, void* mid, size_t count,
+                         hipStream_t st);
+hipError_t launch_quant_rowwise(int fmt, const float* w, int rows, int k, uint8_t* q, float* scale,
+                                hipStream_t st);
+hipError_t launch_quant_int4_g32(const float* w, size_t rows, size_t k, uint8_t* q,
+                                 uint16_t* scales, hipStream_t st);
+hipError_t launch_quant_act_int8(const void* x, int x_dtype, int rows, int k, int8_t* q,
+                                 float* scale, hipStream_t st);
+hipError_t launch_fill_normal(void* dst, int dtype, size_t n, uint64_t seed, float mean,
+                              float stddev, hipStream_t st);
+
+// ---- half-activation GEMM family (mx_gemm_h.hip) --------------------------
+// B operand encodings of the tiled fp16-MFMA GEMM.
+enum BKind : int {
+  BK_F16 = 0,      // f16 [N][K]
+  BK_MXFP4 = 1,    // E2M1 [N][K/2] + E8M0 [N][K/32]
+  BK_E4M3 = 2,     // FP8 E4M3 [N][K] + f32 row scale [N]
+  BK_E5M2 = 3,     // FP8 E5M2 [N][K] + f32 row scale [N]
+  BK_INT8 = 4,     // int8 [N][K] + f32 row scale [N]
+  BK_INT4G32 = 5,  // int4 [N][K/2] + f16 scale [N][K/32]
+};
+
+// Epilogues.
+enum Epi : int {
+  EPI_STORE_F32 = 0,     // C f32 [M][N]
+  EPI_STORE_F16 = 1,     // C f16 [M][N]
+  EPI_SWIGLU_F16 = 2,    // dual B: mid f16 = silu(g) * u              (swiglu_float)
+  EPI_SWIGLU_HALF = 3,   // dual B: mid f16 = silu(clamp(g/16)) * u/16  (swiglu_half)
+};
+
+struct GemmArgs {
+  const void* a;  int a_dtype;            // f16 or f32 [M][K]
+  const void* b0; const void* s0;         // weights + scales (matrix 0)
+  const void* b1; const void* s1;         // second matrix for dual epilogues
+  void* c;                                // output
+  int m, n, k;                            // n = columns of each B matrix
+};
+
+hipError_t launch_gemm_h(int bkind, int epi, const GemmArgs& g, hipStream_t st);
+
+// Decode-shaped (tokens <= 16) split-K GEMV family (mx_gemv.hip).
+struct GemvArgs {
+  const uint16_t* x;                      // f16 [T][K]
+  const uint8_t* b0; const uint8_t* s0;   // MXFP4 weights (matrix 0)
+  const uint8_t* b1; const uint8_t* s1;   // second matrix (dual / SwiGLU)
+  uint16_t* out;                          // f16 [T][N] (out or mid)
+  float* partial;                         // [splits][T][N * nb] workspace
+  uint32_t* counters;                     // [N/16] zero-initialised, self-resetting
+  int t, n, k, splits;
+};
+hipError_t launch_gemv_mxfp4(int dual_swiglu, const GemvArgs& g, hipStream_t st);
+int gemv_pick_splits(int n, int k, int dual);
+size_t gemv_partial_floats(int t, int n, int splits, int dual);
+
+// W4A4 FP4 x FP4 scaled-MFMA GEMM (mx_gemm_fp4.hip).
+struct Fp4GemmArgs {
+  const uint8_t* a; const uint8_t* as;    // activations MXFP4 [M][K/2], [M][K/32]
+  const uint8_t* b0; const uint8_t* s0;   // weights MXFP4 [N][K/2], [N][K/32]
+  const uint8_t* b1; const uint8_t* s1;   // up weights (dual epilogue)
+  void* c;                                // f16 [M][N] or mid MXFP4 [M][N/2]
+  uint8_t* cs;                            // mid scales [M][N/32] (dual epilogue)
+  int m, n, k;
+};
+hipError_t launch_gemm_fp4(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+
+}  // namespace mx

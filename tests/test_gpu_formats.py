@@ -1,0 +1,73 @@
+"""GPU parity of the weight-format rows.
+
+Reference rows: mpp_mlp_h_fp8e4m3_f / _h_fp8e5m2_f / _h_i8_f / _h_i4_f /
+i8_i8_i32 (MPPMLPKernels.metal:50-125), unscaled in the reference; BASELINE
+adds per-row (FP8, INT8) and per-32 f16 (INT4) scales.  Quantizers must be
+bit-exact with the oracle; MLP outputs within the BASELINE tolerance.
+"""
+import numpy as np
+import pytest
+
+import mxfp4hip as M
+import oracle as O
+from mlp_data import MlpData, sample_rows
+
+pytestmark = pytest.mark.gpu
+FMTS = [M.WFMT_FP8_E4M3, M.WFMT_FP8_E5M2, M.WFMT_INT8, M.WFMT_INT4]
+
+
+@pytest.mark.parametrize("wfmt", FMTS)
+def test_format_quantizer_bitexact(dev, wfmt):
+    rng = np.random.default_rng(wfmt)
+    rows, k = 96, 1024
+    w = rng.normal(0, 0.02, (rows, k)).astype(np.float32)
+    w[3] *= 1e4
+    w[5, :64] = 0
+    dw = dev.upload(w)
+    if wfmt == M.WFMT_INT4:
+        q, s = dev.alloc(rows * k // 2), dev.alloc(rows * k // 32 * 2)
+        dev.fmt_quantize(wfmt, dw, rows, k, q, s)
+        oq, os_ = O.quant_int4_g32(w)
+        assert np.array_equal(dev.download(s, np.uint16, (rows, k // 32)), os_.view(np.uint16))
+        assert np.array_equal(dev.download(q, np.uint8, (rows, k // 2)), oq)
+    else:
+        q, s = dev.alloc(rows * k), dev.alloc(rows * 4)
+        dev.fmt_quantize(wfmt, dw, rows, k, q, s)
+        oq, os_ = O.quant_rowwise(wfmt, w)
+        assert np.array_equal(dev.download(s, np.float32, (rows,)), os_)
+        assert np.array_equal(dev.download(q, np.uint8, (rows, k)), oq)
+
+
+def run_fmt(dev, d, wfmt):
+    out = dev.alloc(d.T * d.H * 2)
+    dev.fmt_mlp_forward(wfmt, d.T, d.H, d.I, d.x, d.weights, out)
+    got = dev.download(out, np.float16, (d.T, d.H))
+    out.free()
+    return got
+
+
+def oracle_fmt(d, wfmt, rows=None):
+    x, ((qg, sg), (qu, su), (qd, sd)) = d.host()
+    return O.mlp_format(wfmt, x, qg, sg, qu, su, qd, sd, d.H, d.I, rows=rows, threads=16)
+
+
+@pytest.mark.parametrize("wfmt", FMTS)
+@pytest.mark.parametrize("T", [3, 128])
+def test_format_mlp_small(dev, wfmt, T):
+    d = MlpData(dev, T, 512, 1024, seed=wfmt * 10 + T, wfmt=wfmt)
+    got = run_fmt(dev, d, wfmt)
+    rel, cos = O.mlp_error(got, oracle_fmt(d, wfmt))
+    print(f"fmt {wfmt} T={T}: rel={rel:.3e} cos={cos:.7f}", flush=True)
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    d.free()
+
+
+@pytest.mark.parametrize("wfmt", FMTS)
+def test_config3_formats(dev, wfmt):
+    d = MlpData(dev, 128, 4096, 14336, seed=31 + wfmt, wfmt=wfmt)
+    rows = sample_rows(128, 16)
+    got = run_fmt(dev, d, wfmt)[rows]
+    rel, cos = O.mlp_error(got, oracle_fmt(d, wfmt, rows=rows))
+    print(f"C3 fmt {wfmt}: rel={rel:.3e} cos={cos:.7f}", flush=True)
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    d.free()

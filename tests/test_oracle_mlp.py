@@ -1,0 +1,196 @@
+"""Pin the CPU oracle's quantizer, dequant, matmul and MLP (CPU only).
+
+Pins:
+  * the reference's published checksum 403573 of its native scale-plane rows
+    (README.md:292-294), recomputed from the reference's own data recipe
+    (main.swift:611-638) - this fixes layouts, nibble order, scale indexing,
+    the swiglu_half epilogue and the LCG generators at once;
+  * quantizer invariants that follow from the BASELINE definition;
+  * independent float64 numpy evaluation of the matmul and the MLP;
+  * the committed tiny-MLP fixture (regression).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+FP4 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0,
+                -6.0])
+
+
+def deq_np(q, s, k):
+    codes = np.stack([q & 15, q >> 4], -1).reshape(q.shape[0], k)
+    return FP4[codes] * np.repeat(2.0 ** (s.astype(np.float64) - 127), 32, axis=1)
+
+
+def test_reference_checksum_403573():
+    kat = json.load(open(os.path.join(GOLD, "checksum_kat.json")))
+    T, H, I = kat["tokens"], kat["hidden"], kat["intermediate"]
+    x = O.lcg_half(kat["x"]["seed"], T * H, kat["x"]["scale"]).reshape(T, H)
+    wg = O.lcg_bytes(kat["fp4"]["gate"], I * H // 2).reshape(I, H // 2)
+    wu = O.lcg_bytes(kat["fp4"]["up"], I * H // 2).reshape(I, H // 2)
+    wd = O.lcg_bytes(kat["fp4"]["down"], H * I // 2).reshape(H, I // 2)
+    pat = kat["e8m0"]["pattern"]
+    sg = O.lcg_pattern(kat["e8m0"]["gate"], I * H // 32, pat).reshape(I, H // 32)
+    su = O.lcg_pattern(kat["e8m0"]["up"], I * H // 32, pat).reshape(I, H // 32)
+    sd = O.lcg_pattern(kat["e8m0"]["down"], H * I // 32, pat).reshape(H, I // 32)
+    out = O.mlp_mxfp4(O.MLP_REFROW, x, wg, sg, wu, su, wd, sd, H, I, threads=8)
+    s, n = O.checksum_f32(out)
+    assert n == kat["samples"]
+    assert "%.6g" % s == kat["checksum"]
+
+
+def test_quantizer_invariants():
+    rng = np.random.default_rng(1)
+    w = rng.normal(0, 0.02, (256, 1024)).astype(np.float32)
+    q, s = O.mxfp4_quantize(w)
+    assert set(np.unique(s)) <= {119, 120, 121}        # N(0,0.02) block amax range
+    codes = np.stack([q & 15, q >> 4], -1).reshape(256, 1024)
+    mags = (codes & 7).reshape(256, 32, 32).max(axis=2)
+    assert set(np.unique(mags)) <= {6, 7}              # block max encodes to 4 or 6
+    d = deq_np(q, s, 1024)
+    scale = np.repeat(2.0 ** (s.astype(np.float64) - 127), 32, axis=1)
+    err = np.abs(d - w) / scale
+    # half an E2M1 ulp: 0.25 below 2, 0.5 in [2,4), 1.0 in [4,6]; saturation above 6
+    a = np.abs(w) / scale
+    bound = np.where(a < 2, 0.25, np.where(a < 4, 0.5, 1.0))
+    sat = a > 6
+    assert np.all(err[~sat] <= bound[~sat] + 1e-12)
+    assert np.all(np.abs(d[sat]) == 6 * scale[sat])
+    # scale definition: amax in [4, 8) * 2^(byte-127)
+    amax = np.abs(w).reshape(256, 32, 32).max(axis=2)
+    ratio = amax / 2.0 ** (s.astype(np.float64) - 127)
+    assert np.all((ratio >= 4) & (ratio < 8))
+
+
+def test_quantizer_special_blocks():
+    L = O.lib()
+    assert L.orc_mxfp4_scale_byte(0.0) == 127
+    assert L.orc_mxfp4_scale_byte(float("inf")) == 255
+    assert L.orc_mxfp4_scale_byte(1.0) == 125        # 2^(0-2)
+    assert L.orc_mxfp4_scale_byte(7.99) == 127
+    assert L.orc_mxfp4_scale_byte(8.0) == 128
+    assert L.orc_mxfp4_scale_byte(1e-45) == 0        # subnormal amax clamps
+    blk = np.zeros((1, 32), np.float32)
+    blk[0, 3] = np.nan
+    q, s = O.mxfp4_quantize(blk)
+    assert s[0, 0] == 255 and not q.any()
+
+
+def test_dequant_closed_form_all_codes_scales():
+    # every (code, scale byte) pair: 16 codes x 256 scales
+    q = np.tile(np.array([0x10, 0x32, 0x54, 0x76, 0x98, 0xba, 0xdc, 0xfe] * 2, np.uint8), (256, 1))
+    s = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    out = O.mxfp4_dequant_f16(q, s, 256, 32)
+    codes = np.stack([q & 15, q >> 4], -1).reshape(256, 32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = (FP4[codes].astype(np.float32) *
+                np.array([O.lib().orc_e8m0_to_float(b) for b in range(256)], np.float32)[:, None])
+        want = want.astype(np.float16)
+    same = (out.view(np.uint16) == want.view(np.uint16)) | (np.isnan(out) & np.isnan(want))
+    assert same.all()
+
+
+def test_matmul_vs_numpy_float64():
+    rng = np.random.default_rng(2)
+    M, N, K = 5, 96, 256
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    q = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    s = rng.integers(120, 134, (N, K // 32), dtype=np.uint8)
+    got = O.mxfp4_matmul(a, q, s, N)
+    want = a.astype(np.float64) @ deq_np(q, s, K).T
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+    # all scales = 127 reduces to a plain fp16 GEMM
+    s1 = np.full_like(s, 127)
+    got1 = O.mxfp4_matmul(a, q, s1, N)
+    w = FP4[np.stack([q & 15, q >> 4], -1).reshape(N, K)].astype(np.float16)
+    np.testing.assert_allclose(got1, a.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-6,
+                               atol=1e-6)
+    # linearity in the activations (power-of-two scaling is exact)
+    got2 = O.mxfp4_matmul((a.astype(np.float32) * 4).astype(np.float16), q, s, N)
+    np.testing.assert_array_equal(got2, got * 4)
+
+
+def test_tiny_mlp_fixture_and_independent_eval():
+    z = np.load(os.path.join(GOLD, "tiny_mlp.npz"))
+    H, I = z["x"].shape[1], z["qg"].shape[0]
+    args = (z["x"], z["qg"], z["sg"], z["qu"], z["su"], z["qd"], z["sd"], H, I)
+    out = O.mlp_mxfp4(O.MLP_F16, *args)
+    assert np.array_equal(out.view(np.uint16), z["out_f16"].view(np.uint16))
+    assert np.array_equal(O.mlp_mxfp4(O.MLP_W4A4, *args).view(np.uint16), z["out_w4a4"].view(np.uint16))
+    assert np.array_equal(O.mlp_mxfp4(O.MLP_REFROW, *args), z["out_ref"])
+    # independent float64 evaluation agrees to f16 rounding
+    np.testing.assert_allclose(out.astype(np.float64), z["out_f64"], rtol=2e-3, atol=1e-4)
+    # W4A4 quantizes x and mid to 4 bits: it tracks the f16-activation MLP
+    # only loosely (its parity is against the W4A4 oracle, not this one)
+    rel, cos = O.mlp_error(z["out_w4a4"], z["out_f64"])
+    assert 0.9 < cos < 0.9995
+
+
+def test_row_selection_matches_full():
+    z = np.load(os.path.join(GOLD, "tiny_mlp.npz"))
+    H, I = z["x"].shape[1], z["qg"].shape[0]
+    args = (z["x"], z["qg"], z["sg"], z["qu"], z["su"], z["qd"], z["sd"], H, I)
+    full = O.mlp_mxfp4(O.MLP_F16, *args)
+    one = O.mlp_mxfp4(O.MLP_F16, *args, rows=[1], threads=3)
+    assert np.array_equal(one.view(np.uint16), full[1:2].view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt", [O.WF_E4M3, O.WF_E5M2, O.WF_INT8])
+def test_rowwise_format_quantizers(fmt):
+    rng = np.random.default_rng(fmt)
+    w = rng.normal(0, 0.02, (64, 256)).astype(np.float32)
+    q, sc = O.quant_rowwise(fmt, w)
+    qmax = {O.WF_E4M3: 448.0, O.WF_E5M2: 57344.0, O.WF_INT8: 127.0}[fmt]
+    np.testing.assert_array_equal(sc, (np.abs(w).max(1) / np.float32(qmax)).astype(np.float32))
+    if fmt == O.WF_INT8:
+        v = q.view(np.int8).astype(np.float64)
+        want = np.clip(np.rint(w / sc[:, None]), -127, 127)
+        np.testing.assert_array_equal(v, want)
+    else:
+        dec = O.unpack(O.FMT_E4M3 if fmt == O.WF_E4M3 else O.FMT_E5M2, q.reshape(-1), q.size)
+        rel = np.abs(dec.reshape(q.shape) * sc[:, None] - w) / np.abs(w).max(1, keepdims=True)
+        assert rel.max() < (2 ** -4 if fmt == O.WF_E4M3 else 2 ** -3)
+
+
+def test_int4_g32_quantizer():
+    rng = np.random.default_rng(9)
+    w = rng.normal(0, 0.02, (16, 128)).astype(np.float32)
+    q, sc = O.quant_int4_g32(w)
+    codes = np.stack([q & 15, q >> 4], -1).reshape(16, 128).astype(np.int64)
+    vals = (codes ^ 8) - 8
+    s = np.repeat(sc.astype(np.float32), 32, axis=1)
+    np.testing.assert_array_equal(vals, np.clip(np.rint(w / s), -8, 7))
+    amax = np.abs(w).reshape(16, 4, 32).max(2)
+    np.testing.assert_array_equal(sc, (amax / np.float32(7)).astype(np.float16))
+
+
+def test_format_mlp_vs_numpy():
+    rng = np.random.default_rng(11)
+    T, H, I = 3, 64, 96
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    ws = [rng.normal(0, 0.02, s).astype(np.float32) for s in ((I, H), (I, H), (H, I))]
+    for fmt in (O.WF_E4M3, O.WF_E5M2, O.WF_INT8, O.WF_INT4, O.WF_W8A8):
+        if fmt == O.WF_INT4:
+            qs = [O.quant_int4_g32(w) for w in ws]
+            deq = [((np.stack([q & 15, q >> 4], -1).reshape(w.shape).astype(np.int64) ^ 8) - 8) *
+                   np.repeat(s.astype(np.float64), 32, axis=1) for (q, s), w in zip(qs, ws)]
+        else:
+            qs = [O.quant_rowwise(O.WF_INT8 if fmt == O.WF_W8A8 else fmt, w) for w in ws]
+            if fmt in (O.WF_INT8, O.WF_W8A8):
+                deq = [q.view(np.int8).astype(np.float64) * s[:, None].astype(np.float64) for q, s in qs]
+            else:
+                f = O.FMT_E4M3 if fmt == O.WF_E4M3 else O.FMT_E5M2
+                deq = [O.unpack(f, q.reshape(-1), q.size).reshape(q.shape).astype(np.float64) *
+                       s[:, None] for q, s in qs]
+        out = O.mlp_format(fmt, x, qs[0][0], qs[0][1], qs[1][0], qs[1][1], qs[2][0], qs[2][1], H, I)
+        xf = x.astype(np.float64)
+        g, u = xf @ deq[0].T, xf @ deq[1].T
+        ref = (g / (1 + np.exp(-g)) * u) @ deq[2].T
+        rel, cos = O.mlp_error(out, ref)
+        tol = 5e-2 if fmt == O.WF_W8A8 else O.MAX_ABS_REL_TOL
+        assert rel <= tol and cos >= 0.999, (fmt, rel, cos)
