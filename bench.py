@@ -1,0 +1,200 @@
+"""Benchmark of the MXFP4 MLP hot path on one MI355X (prints one JSON line).
+
+Workload (the decode-shaped MLP the north star's
+HBM target is quoted on): tokens=1, hidden=7168, intermediate=2048, x ~ f16
+N(0,1), weights N(0,0.02) quantized to MXFP4 (E2M1 + E8M0 per 32 K), 24
+distinct weight sets rotated inside the timed loop (2.2x the 256 MB
+last-level cache, as for MoE experts).  One step = one full MLP forward
+down(silu(gate(x)) * up(x)).
+
+Secondary measurements (configs 0, 1 with T=8, 2, 3 and 4) are reported in
+the same JSON line under "secondary"; they are not the headline value.
+
+  value        effective TFLOP/s = 6*T*H*I / (time per step)
+  roofline     the dominant kernel (fused gate/up GEMV): algorithmic bytes per
+               launch / its average launch time from HIP events on the
+               library stream, against 8 TB/s
+  cpu_baseline the CPU oracle (a scalar C port of the reference's
+               dequantize-then-accumulate MLP) on the host cores, same inputs
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mpp-4.1-fp4-fp8-block_amd"))
+
+HBM_PEAK = 8.0e12            # B/s
+PEAK = {"fp4": 10.1e15, "fp8": 5.0e15, "f16": 2.5e15, "i8": 5.0e15}
+METRIC = "MXFP4 MLP µs/iter + effective TFLOP/s (1×MI355X), % of MFMA/HBM roofline"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def mxfp4_bytes(n, k):
+    return n * k // 2 + n * k // 32
+
+
+def make_sets(dev, M, T, H, I, n_sets, seed, wfmt=0):
+    """x (f16) and n_sets weight sets, all generated and quantized on the GPU."""
+    x = dev.alloc(T * H * 2)
+    dev.fill_normal(x, M.DT_F16, T * H, seed, 0.0, 1.0)
+    tmp = dev.alloc(max(I * H, H * I) * 4)
+    sets, bufs = [], []
+    for s in range(n_sets):
+        mats = []
+        for j, (n, k) in enumerate(((I, H), (I, H), (H, I))):
+            dev.fill_normal(tmp, M.DT_F32, n * k, seed * 100 + s * 3 + j + 1, 0.0, 0.02)
+            if wfmt == 0:
+                q, sc = dev.alloc(n * k // 2), dev.alloc(n * k // 32)
+                dev.mxfp4_quantize(tmp, M.DT_F32, n, k, q, sc)
+            else:
+                qb = n * k // 2 if wfmt == M.WFMT_INT4 else n * k
+                sb = n * (k // 32) * 2 if wfmt == M.WFMT_INT4 else n * 4
+                q, sc = dev.alloc(qb), dev.alloc(sb)
+                dev.fmt_quantize(wfmt, tmp, n, k, q, sc)
+            mats.append((q, sc))
+            bufs += [q, sc]
+        sets.append(M.Device.weights(*mats))
+    tmp.free()
+    dev.sync()
+    return x, sets, bufs
+
+
+def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt=0):
+    x, sets, bufs = make_sets(dev, M, T, H, I, n_sets, seed, wfmt)
+    out = dev.alloc(T * H * 4)
+    if wfmt:
+        secs = dev.fmt_mlp_benchmark(wfmt, T, H, I, x, sets, out, warmup=warmup, iterations=iters)
+        kern = {}
+    else:
+        secs, kern = dev.mlp_benchmark(variant, T, H, I, x, sets, out, warmup=warmup,
+                                       iterations=iters)
+    us = secs / iters * 1e6
+    flops = 6.0 * T * H * I
+    res = {"tokens": T, "hidden": H, "intermediate": I, "weight_sets": n_sets, "iters": iters,
+           "us_per_iter": round(us, 3), "tflops": round(flops / (us * 1e-6) / 1e12, 3),
+           "kernel_us": {k: round(v, 3) for k, v in kern.items()}}
+    for b in bufs + [x, out]:
+        b.free()
+    log(f"[bench] {name}: {us:.2f} us/iter, {res['tflops']} TFLOP/s, kernels {res['kernel_us']}")
+    return res, (x, sets)
+
+
+def cpu_baseline(T, H, I, budget_s=12.0):
+    """Time the CPU oracle's MLP (f16 activations, MXFP4 weights) on host
+    cores, on the same shapes with data generated on the host."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    qs = []
+    for n, k in ((I, H), (I, H), (H, I)):
+        w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+        qs += list(O.mxfp4_quantize(w))
+    O.mlp_mxfp4(O.MLP_F16, x, *qs, H, I, threads=threads)      # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.mlp_mxfp4(O.MLP_F16, x, *qs, H, I, threads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 400:
+            break
+    us = el / n * 1e6
+    return {"value": round(6.0 * T * H * I / (us * 1e-6) / 1e12, 6), "unit": "TFLOP/s",
+            "us_per_iter": round(us, 1), "cores": threads, "kind": "port",
+            "sample": f"{n} full MLP forwards at T={T} H={H} I={I} (oracle/mx_oracle.c, "
+                      f"float64 accumulation, {threads} threads), ~{el:.0f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(the MXFP4 MLP hot path is a single-GPU kernel; see DESIGN.md for how it shards).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import mxfp4hip as M
+    dev = M.Device(0)
+    name, cus, clk = dev.info()
+    log(f"[bench] device {name}, {cus} CUs, {clk} MHz")
+
+    # ---- headline: config 1, T=1 ------------------------------------------
+    T, H, I = 1, 7168, 2048
+    prim, _ = run_config(dev, M, "C1 T=1 fused", M.MLP_FUSED, T, H, I, 24, args.steps,
+                         args.warmup, seed=1)
+    us = prim["us_per_iter"]
+    gu_name = "gemv_mxfp4_gate_up_swiglu"
+    gu_us = prim["kernel_us"][gu_name]
+    gu_bytes = 2 * mxfp4_bytes(I, H) + T * H * 2 + T * I * 2
+    mlp_bytes = 3 * mxfp4_bytes(I, H) + 2 * T * H * 2 + 2 * T * I * 2
+    achieved = gu_bytes / (gu_us * 1e-6)
+    roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                "kernel": gu_name, "algorithmic_bytes": gu_bytes,
+                "kernel_us": round(gu_us, 3)}
+    result = {
+        "metric": METRIC, "value": prim["tflops"], "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 6),
+        "us_per_iter": us, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "BASELINE configs[1] decode MLP, tokens=1 hidden=7168 "
+                               "intermediate=2048, MXFP4 weights, 24 rotated weight sets",
+                   "tokens": T, "hidden": H, "intermediate": I, "weight_sets": 24,
+                   "variant": "fused (split-K GEMV, in-register FP4 decode, fp16 MFMA)"},
+        "mlp_hbm_gbps": round(mlp_bytes / (us * 1e-6) / 1e9, 1),
+        "mlp_hbm_frac": round(mlp_bytes / (us * 1e-6) / HBM_PEAK, 4),
+        "kernel_us": prim["kernel_us"],
+        "roofline": roofline,
+    }
+
+    if not args.no_secondary:
+        sec = {}
+        r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2)
+        b = 3 * mxfp4_bytes(2048, 7168) + 2 * 8 * 7168 * 2 + 2 * 8 * 2048 * 2
+        r["hbm_frac"] = round(b / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
+        sec["c1_t8_fused"] = r
+        r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, 1, 10, 2, seed=4)
+        r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
+        sec["c4_w4a4"] = r
+        for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_W4A4, "w4a4")):
+            r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, 24, 100, 10, seed=5)
+            sec[f"c0_{tag}"] = r
+        for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant")):
+            r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, 24, 100, 10, seed=6)
+            r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
+            sec[f"c2_{tag}"] = r
+        for wfmt, tag in ((M.WFMT_FP8_E4M3, "fp8_e4m3"), (M.WFMT_FP8_E5M2, "fp8_e5m2"),
+                          (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32")):
+            r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, 2, 40, 4, seed=7,
+                              wfmt=wfmt)
+            wb = 3 * 4096 * 14336 * (0.5 if wfmt == M.WFMT_INT4 else 1)
+            r["hbm_frac"] = round(wb / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
+            sec[f"c3_{tag}"] = r
+        result["secondary"] = sec
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(T, H, I)
+    dev.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
