@@ -70,22 +70,32 @@ def make_sets(dev, M, T, H, I, n_sets, seed, wfmt=0):
 
 
 def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt=0):
+    """Time `iters` forwards twice: replayed from one HIP graph (the value;
+    the reference likewise pre-encodes all iterations in one command buffer)
+    and launched one by one on the stream (reported as stream_us_per_iter)."""
     x, sets, bufs = make_sets(dev, M, T, H, I, n_sets, seed, wfmt)
     out = dev.alloc(T * H * 4)
     if wfmt:
-        secs = dev.fmt_mlp_benchmark(wfmt, T, H, I, x, sets, out, warmup=warmup, iterations=iters)
+        secs = dev.fmt_mlp_benchmark(wfmt, T, H, I, x, sets, out, warmup=warmup, iterations=iters,
+                                     graph=True)
+        ssecs = dev.fmt_mlp_benchmark(wfmt, T, H, I, x, sets, out, warmup=0, iterations=iters,
+                                      graph=False)
         kern = {}
     else:
         secs, kern = dev.mlp_benchmark(variant, T, H, I, x, sets, out, warmup=warmup,
-                                       iterations=iters)
+                                       iterations=iters, graph=True)
+        ssecs, _ = dev.mlp_benchmark(variant, T, H, I, x, sets, out, warmup=0,
+                                     iterations=iters, per_kernel=False, graph=False)
     us = secs / iters * 1e6
     flops = 6.0 * T * H * I
     res = {"tokens": T, "hidden": H, "intermediate": I, "weight_sets": n_sets, "iters": iters,
            "us_per_iter": round(us, 3), "tflops": round(flops / (us * 1e-6) / 1e12, 3),
+           "stream_us_per_iter": round(ssecs / iters * 1e6, 3),
            "kernel_us": {k: round(v, 3) for k, v in kern.items()}}
     for b in bufs + [x, out]:
         b.free()
-    log(f"[bench] {name}: {us:.2f} us/iter, {res['tflops']} TFLOP/s, kernels {res['kernel_us']}")
+    log(f"[bench] {name}: {us:.2f} us/iter (stream {res['stream_us_per_iter']}), "
+        f"{res['tflops']} TFLOP/s, kernels {res['kernel_us']}")
     return res, (x, sets)
 
 

@@ -166,14 +166,17 @@ int mx_mlp_forward(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const voi
 /* Timed loop as runMXFP4FusedMLPBenchmarkVariant (main.swift:1953-2031):
  * `warmup` untimed iterations, then `iterations` back-to-back forwards on the
  * stream between two HIP events.  Iteration i uses weight set i % n_sets
- * (MoE-style rotation; defeats the 256 MB last-level cache).
+ * (MoE-style rotation; defeats the 256 MB last-level cache).  use_graph != 0
+ * captures the `iterations` forwards into one HIP graph and times one replay
+ * (the reference likewise encodes all iterations into one command buffer,
+ * main.swift:2062-2117); 0 launches them one by one.
  * seconds_out: total timed seconds.  kernel_us_out (optional, length
  * >= 8): average device time per iteration of each kernel of the forward, in
  * launch order, from events around each launch in a second timed pass;
  * n_kernels_out: how many were written. */
 int mx_mlp_benchmark(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const void* x,
                      const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
-                     int iterations, double* seconds_out, double* kernel_us_out,
+                     int iterations, int use_graph, double* seconds_out, double* kernel_us_out,
                      int* n_kernels_out);
 /* Name of kernel `index` of a variant's forward (for the per-kernel times). */
 const char* mx_mlp_kernel_name(int variant, int tokens, int index);
@@ -188,7 +191,7 @@ int mx_fmt_mlp_forward(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const vo
                        const mx_mlp_weights* w, void* out);
 int mx_fmt_mlp_benchmark(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,
                          const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
-                         int iterations, double* seconds_out);
+                         int iterations, int use_graph, double* seconds_out);
 
 /* ---- synthetic data (main.swift:2785-2842) ---------------------------------- */
 /* Seeded N(mean, std) on the device (f32 or f16). */

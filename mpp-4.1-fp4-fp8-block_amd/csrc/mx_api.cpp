@@ -22,15 +22,12 @@ struct mx_ctx {
   std::string err;
   char name[256] = {0};
   int cus = 0, clock_mhz = 0;
-  // scratch owned by the context (grown on demand; counters zeroed once)
+  // scratch owned by the context (grown on demand)
   void* ws = nullptr;
   size_t ws_bytes = 0;
-  uint32_t* counters = nullptr;  // two regions of kMaxCounters
 };
 
 namespace {
-
-constexpr size_t kMaxCounters = 1 << 16;  // row groups per GEMV phase
 
 int set_err(mx_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -70,18 +67,6 @@ int ensure_ws(mx_ctx* c, size_t bytes) {
   return MX_OK;
 }
 
-int ensure_counters(mx_ctx* c) {
-  if (c->counters) return MX_OK;
-  if (hipMalloc(reinterpret_cast<void**>(&c->counters), 2 * kMaxCounters * sizeof(uint32_t)) !=
-      hipSuccess) {
-    c->counters = nullptr;
-    return set_err(c, MX_ENOMEM, "Could not create device buffer counters.");
-  }
-  MX_HIP(c, hipMemsetAsync(c->counters, 0, 2 * kMaxCounters * sizeof(uint32_t), c->stream));
-  MX_HIP(c, hipStreamSynchronize(c->stream));
-  return MX_OK;
-}
-
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // A forward pass as a list of launches (so the benchmark can time each).
@@ -110,14 +95,17 @@ int check_mlp_cfg(mx_ctx* c, int variant, const mx_mlp_config* cfg) {
 }
 
 bool gemv_ok(const mx_mlp_config* cfg) {
+  // decode GEMV: <= 16 tokens, K multiples of 128, and the activations plus
+  // one row group's scales fit the workgroup's LDS
   return cfg->tokens <= 16 && cfg->hidden % 128 == 0 && cfg->intermediate % 128 == 0 &&
-         cfg->hidden / 16 <= kMaxCounters && cfg->intermediate / 16 <= kMaxCounters;
+         mx::gemv_lds_need((int)cfg->tokens, (int)cfg->hidden) <= 160 * 1024 &&
+         mx::gemv_lds_need((int)cfg->tokens, (int)cfg->intermediate) <= 160 * 1024;
 }
 
 // Scratch layout for one variant; returns bytes needed.
 struct MlpScratch {
   size_t mid = 0, gate = 0, up = 0, wg = 0, wu = 0, wd = 0, xq = 0, xs = 0, mq = 0, ms = 0;
-  size_t part = 0, total = 0;
+  size_t total = 0;
 };
 
 MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
@@ -127,13 +115,6 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
   if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
     s.mid = take(T * I * 2);
-    if (variant == MX_MLP_FUSED && gemv_ok(cfg)) {
-      const int sp_gu = mx::gemv_pick_splits((int)I, (int)H, 1);
-      const int sp_d = mx::gemv_pick_splits((int)H, (int)I, 0);
-      size_t p = mx::gemv_partial_floats((int)T, (int)I, sp_gu, 1);
-      size_t p2 = mx::gemv_partial_floats((int)T, (int)H, sp_d, 0);
-      s.part = take((p > p2 ? p : p2) * 4);
-    }
   } else if (variant == MX_MLP_DEQUANT) {
     s.wg = take(I * H * 2);
     s.wu = take(I * H * 2);
@@ -160,14 +141,13 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
   for (const mx_qmatrix* m : mats) {
     if (!m->data || !m->scales) return set_err(c, MX_EINVAL, "MLP weight buffers must not be null.");
     if (!aligned16(m->data)) return set_err(c, MX_EINVAL, "MXFP4 weight data must be 16-byte aligned.");
-    if (variant == MX_MLP_W4A4 && (reinterpret_cast<uintptr_t>(m->scales) & 3u))
-      return set_err(c, MX_EINVAL, "W4A4 scale planes must be 4-byte aligned.");
+    if (reinterpret_cast<uintptr_t>(m->scales) & 3u)
+      return set_err(c, MX_EINVAL, "MXFP4 scale planes must be 4-byte aligned.");
   }
   if (!aligned16(x) || !aligned16(out))
     return set_err(c, MX_EINVAL, "Activation and output buffers must be 16-byte aligned.");
   MlpScratch s = plan_scratch(variant, cfg);
   if ((rc = ensure_ws(c, s.total))) return rc;
-  if ((rc = ensure_counters(c))) return rc;
   uint8_t* ws = static_cast<uint8_t*>(c->ws);
   hipStream_t st = c->stream;
   const int T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
@@ -180,11 +160,8 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
 
   if (variant == MX_MLP_FUSED && gemv_ok(cfg)) {
     uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
-    float* part = reinterpret_cast<float*>(ws + s.part);
-    mx::GemvArgs gu{static_cast<const uint16_t*>(x), wg, sg, wu, su, mid, part, c->counters,
-                    T, I, H, mx::gemv_pick_splits(I, H, 1)};
-    mx::GemvArgs dn{mid, wd, sd, nullptr, nullptr, static_cast<uint16_t*>(out), part,
-                    c->counters + kMaxCounters, T, H, I, mx::gemv_pick_splits(H, I, 0)};
+    mx::GemvArgs gu{static_cast<const uint16_t*>(x), wg, sg, wu, su, mid, T, I, H};
+    mx::GemvArgs dn{mid, wd, sd, nullptr, nullptr, static_cast<uint16_t*>(out), T, H, I};
     steps.push_back({"gemv_mxfp4_gate_up_swiglu", [=] { return mx::launch_gemv_mxfp4(1, gu, st); }});
     steps.push_back({"gemv_mxfp4_down", [=] { return mx::launch_gemv_mxfp4(0, dn, st); }});
   } else if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
@@ -281,7 +258,6 @@ void mx_destroy(mx_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   if (c->ws) (void)hipFree(c->ws);
-  if (c->counters) (void)hipFree(c->counters);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -496,14 +472,42 @@ const char* mx_mlp_kernel_name(int variant, int tokens, int index) {
   return nullptr;
 }
 
+// Capture `iterations` forwards into one HIP graph (kernel nodes only: no
+// memset or copy nodes) - the counterpart of the reference encoding all
+// iterations into one command buffer (main.swift:2062-2117).
+static int capture_graph(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int iterations,
+                         hipGraphExec_t* exec) {
+  const int ns = (int)sets.size();
+  hipGraph_t graph = nullptr;
+  MX_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  int rc = MX_OK;
+  for (int i = 0; i < iterations && !rc; i++) rc = run_steps(c, sets[i % ns]);
+  hipError_t e = hipStreamEndCapture(c->stream, &graph);
+  if (rc) { if (graph) (void)hipGraphDestroy(graph); return rc; }
+  if (e != hipSuccess) return set_err(c, MX_EGPU, "graph capture failed: %s", hipGetErrorString(e));
+  e = hipGraphInstantiate(exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) return set_err(c, MX_EGPU, "graph instantiate failed: %s", hipGetErrorString(e));
+  return MX_OK;
+}
+
 static int bench_loop(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int warmup,
-                      int iterations, double* seconds_out, double* kernel_us_out,
+                      int iterations, int use_graph, double* seconds_out, double* kernel_us_out,
                       int* n_kernels_out) {
   if (iterations <= 0 || warmup < 0)
     return set_err(c, MX_EINVAL, "MLP sizes and iterations must be positive.");
   const int ns = (int)sets.size();
   for (int i = 0; i < warmup; i++)
     if (int rc = run_steps(c, sets[i % ns])) return rc;
+  hipGraphExec_t gexec = nullptr;
+  if (use_graph) {
+    if (int rc = capture_graph(c, sets, iterations, &gexec)) return rc;
+    // one untimed replay (first launch of an instantiated graph uploads it)
+    if (hipGraphLaunch(gexec, c->stream) != hipSuccess) {
+      (void)hipGraphExecDestroy(gexec);
+      return set_err(c, MX_EGPU, "graph launch failed");
+    }
+  }
   hipEvent_t e0, e1;
   MX_HIP(c, hipEventCreate(&e0));
   MX_HIP(c, hipEventCreate(&e1));
@@ -511,7 +515,11 @@ static int bench_loop(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int
   do {
     if (hipStreamSynchronize(c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "sync failed"); break; }
     if (hipEventRecord(e0, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
-    for (int i = 0; i < iterations && !rc; i++) rc = run_steps(c, sets[i % ns]);
+    if (gexec) {
+      if (hipGraphLaunch(gexec, c->stream) != hipSuccess) rc = set_err(c, MX_EGPU, "graph launch failed");
+    } else {
+      for (int i = 0; i < iterations && !rc; i++) rc = run_steps(c, sets[i % ns]);
+    }
     if (rc) break;
     if (hipEventRecord(e1, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
     if (hipEventSynchronize(e1) != hipSuccess) { rc = set_err(c, MX_EGPU, "MXFP4 MLP timed loop failed."); break; }
@@ -521,6 +529,7 @@ static int bench_loop(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int
   } while (0);
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
+  if (gexec) (void)hipGraphExecDestroy(gexec);
   if (rc) return rc;
   if (kernel_us_out || n_kernels_out) {
     // Second pass: an event before and after every launch.
@@ -556,13 +565,13 @@ static int bench_loop(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int
 
 int mx_mlp_benchmark(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void* x,
                      const mx_mlp_weights* sets, int n_sets, void* out, int warmup, int iterations,
-                     double* seconds_out, double* kernel_us_out, int* n_kernels_out) {
+                     int use_graph, double* seconds_out, double* kernel_us_out, int* n_kernels_out) {
   if (!c) return MX_EINVAL;
   if (!sets || n_sets <= 0) return set_err(c, MX_EINVAL, "benchmark needs at least one weight set.");
   std::vector<std::vector<Step>> all((size_t)n_sets);
   for (int i = 0; i < n_sets; i++)
     if (int rc = build_mlp_steps(c, variant, cfg, x, &sets[i], out, all[i])) return rc;
-  return bench_loop(c, all, warmup, iterations, seconds_out, kernel_us_out, n_kernels_out);
+  return bench_loop(c, all, warmup, iterations, use_graph, seconds_out, kernel_us_out, n_kernels_out);
 }
 
 // ---- weight formats ---------------------------------------------------------------
@@ -625,13 +634,13 @@ int mx_fmt_mlp_forward(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const void
 
 int mx_fmt_mlp_benchmark(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const void* x,
                          const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
-                         int iterations, double* seconds_out) {
+                         int iterations, int use_graph, double* seconds_out) {
   if (!c) return MX_EINVAL;
   if (!sets || n_sets <= 0) return set_err(c, MX_EINVAL, "benchmark needs at least one weight set.");
   std::vector<std::vector<Step>> all((size_t)n_sets);
   for (int i = 0; i < n_sets; i++)
     if (int rc = build_fmt_steps(c, wfmt, cfg, x, &sets[i], out, all[i])) return rc;
-  return bench_loop(c, all, warmup, iterations, seconds_out, nullptr, nullptr);
+  return bench_loop(c, all, warmup, iterations, use_graph, seconds_out, nullptr, nullptr);
 }
 
 // ---- synthetic data ------------------------------------------------------------------

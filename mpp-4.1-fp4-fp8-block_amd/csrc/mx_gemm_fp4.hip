@@ -11,20 +11,23 @@
 // in hardware with no per-block accumulator juggling (the cost the
 // reference's fused per-block form pays, README.md:309-312).
 //
-// Tiling: 256 threads (4 wave64, 2 x 2), workgroup tile 256 (M) x 128 (N
-// rows of B), K stage 128 (two MFMA K-steps of 64).  Each wave owns a
-// 128 x 64 accumulator tile = 4 x 2 MFMA blocks (128 accumulator VGPRs).
-// Operand tiles live in LDS "fragment-major": the 16 bytes lane l feeds to
-// one MFMA sit at offset 16*l of a 1 KB fragment, so every ds_read_b128 is
-// contiguous across the wave and conflict-free, and every global load of a
-// stage writes LDS at 16*thread.  Double-buffered LDS, register prefetch,
-// one barrier per stage.  Scale dwords (4 blocks = 2 K-steps) are loaded
-// per lane and shifted by 8*(lane/32) so that a uniform opsel (byte 0 for
-// K-step 0, byte 2 for K-step 1) picks the lane's own block.
+// Tiling: 256 threads (4 wave64, 2 x 2), workgroup tile 256 (M) x BN (rows
+// of B, 128 or 256), K stage 128 (two MFMA K-steps of 64).  Each wave owns a
+// 128 x BN/2 accumulator tile = 4 x BN/64 MFMA blocks.  Operand tiles live in
+// LDS "fragment-major": the 16 bytes lane l feeds to one MFMA sit at offset
+// 16*l of a 1 KB fragment, so every ds_read_b128 is contiguous across the
+// wave and conflict-free, and every global load of a stage writes LDS at
+// 16*thread.  Double-buffered LDS with register prefetch: the next stage's
+// global loads are in flight during the current stage's MFMAs; one barrier
+// per stage.  All loads are unconditional - rows past M read row M-1 and
+// their results are never stored - because a predicated load makes the
+// compiler wait for it at the join.  Scale dwords (4 blocks = 2 K-steps) are
+// loaded per lane and shifted by 8*(lane/32) so that a uniform opsel (byte 0
+// for K-step 0, byte 2 for K-step 1) picks the lane's own block.
 //
 // Epilogues:
 //   DUAL=false  store C as f16 [M][N]                            (down proj)
-//   DUAL=true   B rows [0,64) are gate rows n0.., [64,128) up rows n0..;
+//   DUAL=true   B rows [0,BN/2) are gate rows, [BN/2,BN) the same up rows;
 //               mid = silu(g) * u is re-quantized to MXFP4 along N (the
 //               next GEMM's K) through LDS: one lane per (row, 32-column
 //               block) computes amax -> E8M0 -> 16 packed bytes + 1 scale.
@@ -38,11 +41,9 @@
 
 namespace mx {
 
-constexpr int kFBM = 256, kFBN = 128, kFBK = 128;  // tile (K in elements)
-constexpr int kAFrag = kFBM / 32 * 2;               // A fragments per stage (8 m-blocks x 2 k-steps)
-constexpr int kBFrag = kFBN / 32 * 2;               // B fragments per stage
-constexpr int kStageBytes = (kAFrag + kBFrag) * 1024;
-constexpr int kMidLdsStride = 33;                   // floats per row in the requant tile
+constexpr int kFBM = 256, kFBK = 128;  // tile M, K per stage (elements)
+constexpr int kAFrag = kFBM / 32 * 2;  // A fragments per stage (8 m-blocks x 2 k-steps)
+constexpr int kMidLdsStride = 33;      // floats per row in the requant tile
 
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   // Hardware deals workgroups round-robin over 8 XCDs.  Give XCD x the
@@ -52,14 +53,18 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return (bid % 8) * per + bid / 8;
 }
 
-template <bool DUAL>
+template <bool DUAL, int BN>
 __global__ __launch_bounds__(256, 1) void k_gemm_fp4(Fp4GemmArgs g) {
+  constexpr int J = BN / 64;               // n-blocks per wave
+  constexpr int BCH = BN / 64;             // B chunks per thread per stage
+  constexpr int kBFrag = BN / 32 * 2;
+  constexpr int kStage = (kAFrag + kBFrag) * 1024;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int M = g.m, K = g.k;
   const int MT = (M + kFBM - 1) / kFBM;
-  const int NT = DUAL ? g.n / (kFBN / 2) : g.n / kFBN;  // tiles along N
+  const int NT = DUAL ? g.n / (BN / 2) : g.n / BN;  // tiles along N
 
   // Tile order: XCD remap, then groups of 8 N-tiles with M fastest inside.
   const int tile = xcd_remap(blockIdx.x, MT * NT);
@@ -70,132 +75,129 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4(Fp4GemmArgs g) {
   const int mt = in_grp / gw, nt = nt_base + in_grp % gw;
   const int m0 = mt * kFBM;
 
-  const size_t a_row_bytes = (size_t)K / 2, row_blocks = (size_t)K / 32;
+  const size_t row_bytes = (size_t)K / 2, row_blocks = (size_t)K / 32;
 
-  // Per-thread global source of each prefetched chunk.
-  // A chunk c = tid + 256u: fragment f = c/64 (m-block f/2, k-step f%2), fl = c%64.
+  // Global source of each chunk this thread stages: chunk c = tid + 256u,
+  // fragment f = c/64 (block f/2, k-step f%2), fragment lane fl = c%64.
   const uint8_t* a_src[4];
-  bool a_ok[4];
 #pragma unroll
   for (int u = 0; u < 4; u++) {
     const int c = tid + 256 * u, f = c >> 6, fl = c & 63;
-    const int row = m0 + (f >> 1) * 32 + (fl & 31);
-    a_ok[u] = row < M;
-    a_src[u] = g.a + (size_t)(a_ok[u] ? row : 0) * a_row_bytes + (f & 1) * 32 + (fl >> 5) * 16;
+    const int row = min(m0 + (f >> 1) * 32 + (fl & 31), M - 1);
+    a_src[u] = g.a + (size_t)row * row_bytes + (f & 1) * 32 + (fl >> 5) * 16;
   }
-  const uint8_t* b_src[2];
+  const uint8_t* b_src[BCH];
 #pragma unroll
-  for (int u = 0; u < 2; u++) {
+  for (int u = 0; u < BCH; u++) {
     const int c = tid + 256 * u, f = c >> 6, fl = c & 63;
-    const int j = f >> 1;  // n-block 0..3
+    const int j = f >> 1;  // n-block of the tile
     const uint8_t* base;
     int row;
     if (DUAL) {
-      base = j < 2 ? g.b0 : g.b1;
-      row = nt * 64 + (j & 1) * 32 + (fl & 31);
+      base = j < J ? g.b0 : g.b1;
+      row = nt * (BN / 2) + (j % J) * 32 + (fl & 31);
     } else {
       base = g.b0;
-      row = nt * kFBN + j * 32 + (fl & 31);
+      row = nt * BN + j * 32 + (fl & 31);
     }
-    b_src[u] = base + (size_t)row * a_row_bytes + (f & 1) * 32 + (fl >> 5) * 16;
+    b_src[u] = base + (size_t)row * row_bytes + (f & 1) * 32 + (fl >> 5) * 16;
   }
-  // Scale sources for this lane's MFMA operands.
-  const int srow_sub = lane & 31, sgrp = lane >> 5;
+  // Scale rows of this lane's MFMA operands.
+  const int srow_sub = lane & 31, shift = 8 * (lane >> 5);
   const uint8_t* as_src[4];
-  bool as_ok[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int row = m0 + wm * 128 + i * 32 + srow_sub;
-    as_ok[i] = row < M;
-    as_src[i] = g.as + (size_t)(as_ok[i] ? row : 0) * row_blocks;
-  }
-  const uint8_t* bs_src[2];
+  for (int i = 0; i < 4; i++)
+    as_src[i] = g.as + (size_t)min(m0 + wm * 128 + i * 32 + srow_sub, M - 1) * row_blocks;
+  const uint8_t* bs_src[J];
+  int bfrag[J];  // which tile n-block feeds the wave's j-th accumulator column
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
+  for (int j = 0; j < J; j++) {
     if (DUAL) {
-      const uint8_t* sb = j == 0 ? g.s0 : g.s1;
-      bs_src[j] = sb + (size_t)(nt * 64 + wn * 32 + srow_sub) * row_blocks;
+      // j < J/2: gate blocks wn*J/2 + j ; j >= J/2: the matching up blocks
+      const int gb = wn * (J / 2) + (j % (J / 2));
+      bfrag[j] = j < J / 2 ? gb : J + gb;
+      const uint8_t* sb = j < J / 2 ? g.s0 : g.s1;
+      bs_src[j] = sb + (size_t)(nt * (BN / 2) + gb * 32 + srow_sub) * row_blocks;
     } else {
-      bs_src[j] = g.s0 + (size_t)(nt * kFBN + wn * 64 + j * 32 + srow_sub) * row_blocks;
+      bfrag[j] = wn * J + j;
+      bs_src[j] = g.s0 + (size_t)(nt * BN + (wn * J + j) * 32 + srow_sub) * row_blocks;
     }
   }
 
-  uint4 ar[4], br[2];
-  uint32_t asr[4], bsr[2];
-  auto load_stage = [&](int kt) {
-    const size_t koff = (size_t)kt * (kFBK / 2);
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      ar[u] = a_ok[u] ? *reinterpret_cast<const uint4*>(a_src[u] + koff) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int u = 0; u < 2; u++) br[u] = *reinterpret_cast<const uint4*>(b_src[u] + koff);
-    const size_t soff = (size_t)kt * 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      asr[i] = as_ok[i] ? *reinterpret_cast<const uint32_t*>(as_src[i] + soff) : 0x7f7f7f7fu;
-#pragma unroll
-    for (int j = 0; j < 2; j++) bsr[j] = *reinterpret_cast<const uint32_t*>(bs_src[j] + soff);
-  };
-  auto store_stage = [&](int buf) {
-    uint8_t* base = smem + buf * kStageBytes;
-#pragma unroll
-    for (int u = 0; u < 4; u++) *reinterpret_cast<uint4*>(base + (tid + 256 * u) * 16) = ar[u];
-#pragma unroll
-    for (int u = 0; u < 2; u++)
-      *reinterpret_cast<uint4*>(base + kAFrag * 1024 + (tid + 256 * u) * 16) = br[u];
-  };
-
-  v16f acc[4][2];
+  v16f acc[4][J];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < J; j++)
 #pragma unroll
       for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
 
   const int KT = K / kFBK;
-  load_stage(0);
-  store_stage(0);
-  uint32_t sa_cur[4], sb_cur[2];
-  const int shift = 8 * sgrp;
+  uint4 ar[4], br[BCH];
+  uint32_t asr[4], bsr[J], sa_cur[4], sb_cur[J];
+
+  // Stage 0.
 #pragma unroll
-  for (int i = 0; i < 4; i++) sa_cur[i] = asr[i] >> shift;
+  for (int u = 0; u < 4; u++) ar[u] = *reinterpret_cast<const uint4*>(a_src[u]);
 #pragma unroll
-  for (int j = 0; j < 2; j++) sb_cur[j] = bsr[j] >> shift;
+  for (int u = 0; u < BCH; u++) br[u] = *reinterpret_cast<const uint4*>(b_src[u]);
+#pragma unroll
+  for (int i = 0; i < 4; i++) sa_cur[i] = *reinterpret_cast<const uint32_t*>(as_src[i]) >> shift;
+#pragma unroll
+  for (int j = 0; j < J; j++) sb_cur[j] = *reinterpret_cast<const uint32_t*>(bs_src[j]) >> shift;
+#pragma unroll
+  for (int u = 0; u < 4; u++) *reinterpret_cast<uint4*>(smem + (tid + 256 * u) * 16) = ar[u];
+#pragma unroll
+  for (int u = 0; u < BCH; u++)
+    *reinterpret_cast<uint4*>(smem + kAFrag * 1024 + (tid + 256 * u) * 16) = br[u];
   __syncthreads();
 
   for (int kt = 0; kt < KT; kt++) {
     const int buf = kt & 1;
-    if (kt + 1 < KT) load_stage(kt + 1);
-    const uint8_t* base = smem + buf * kStageBytes;
+    const bool more = kt + 1 < KT;
+    // Prefetch the next stage (the last stage re-reads itself: unconditional).
+    {
+      const size_t koff = (size_t)(more ? kt + 1 : kt) * (kFBK / 2);
+      const size_t soff = (size_t)(more ? kt + 1 : kt) * 4;
+#pragma unroll
+      for (int u = 0; u < 4; u++) ar[u] = *reinterpret_cast<const uint4*>(a_src[u] + koff);
+#pragma unroll
+      for (int u = 0; u < BCH; u++) br[u] = *reinterpret_cast<const uint4*>(b_src[u] + koff);
+#pragma unroll
+      for (int i = 0; i < 4; i++) asr[i] = *reinterpret_cast<const uint32_t*>(as_src[i] + soff);
+#pragma unroll
+      for (int j = 0; j < J; j++) bsr[j] = *reinterpret_cast<const uint32_t*>(bs_src[j] + soff);
+    }
+    const uint8_t* base = smem + buf * kStage;
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      v4i af[4], bf[2];
+      v4i af[4], bf[J];
 #pragma unroll
       for (int i = 0; i < 4; i++)
         af[i] = *reinterpret_cast<const v4i*>(base + (((wm * 4 + i) * 2 + ks) * 64 + lane) * 16);
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const int jb = DUAL ? (j == 0 ? wn : 2 + wn) : wn * 2 + j;
-        bf[j] = *reinterpret_cast<const v4i*>(base + kAFrag * 1024 + ((jb * 2 + ks) * 64 + lane) * 16);
-      }
+      for (int j = 0; j < J; j++)
+        bf[j] = *reinterpret_cast<const v4i*>(base + kAFrag * 1024 + ((bfrag[j] * 2 + ks) * 64 + lane) * 16);
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < J; j++) {
           if (ks == 0)
             acc[i][j] = mfma_fp4_32x32x64<0, 0>(af[i], bf[j], acc[i][j], (int)sa_cur[i], (int)sb_cur[j]);
           else
             acc[i][j] = mfma_fp4_32x32x64<2, 2>(af[i], bf[j], acc[i][j], (int)sa_cur[i], (int)sb_cur[j]);
         }
     }
-    if (kt + 1 < KT) {
-      store_stage(buf ^ 1);
+    uint8_t* nbase = smem + (buf ^ 1) * kStage;
 #pragma unroll
-      for (int i = 0; i < 4; i++) sa_cur[i] = asr[i] >> shift;
+    for (int u = 0; u < 4; u++) *reinterpret_cast<uint4*>(nbase + (tid + 256 * u) * 16) = ar[u];
 #pragma unroll
-      for (int j = 0; j < 2; j++) sb_cur[j] = bsr[j] >> shift;
-    }
+    for (int u = 0; u < BCH; u++)
+      *reinterpret_cast<uint4*>(nbase + kAFrag * 1024 + (tid + 256 * u) * 16) = br[u];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sa_cur[i] = asr[i] >> shift;
+#pragma unroll
+    for (int j = 0; j < J; j++) sb_cur[j] = bsr[j] >> shift;
     __syncthreads();
   }
 
@@ -204,8 +206,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4(Fp4GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const int col = nt * kFBN + wn * 64 + j * 32 + (lane & 31);
+      for (int j = 0; j < J; j++) {
+        const int col = nt * BN + (wn * J + j) * 32 + (lane & 31);
 #pragma unroll
         for (int v = 0; v < 16; v++) {
           const int row = m0 + wm * 128 + i * 32 + acc32_row(lane, v);
@@ -215,60 +217,66 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4(Fp4GemmArgs g) {
     return;
   }
 
-  // DUAL: mid = silu(gate) * up, staged per wave in LDS (64 rows x 33
-  // floats at a time), then re-quantized to MXFP4 along the channel axis.
+  // DUAL: mid = silu(gate) * up for each of the wave's J/2 channel blocks,
+  // staged per wave in LDS (64 rows x 33 floats at a time), then
+  // re-quantized to MXFP4 along the channel axis.
   float* mid = reinterpret_cast<float*>(smem) + wave * (64 * kMidLdsStride);
   uint8_t* mp = reinterpret_cast<uint8_t*>(g.c);
-  const int chan0 = nt * 64 + wn * 32;          // first channel of this wave's block
   const size_t mid_row_bytes = (size_t)g.n / 2, mid_row_blocks = (size_t)g.n / 32;
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
+  for (int jb = 0; jb < J / 2; jb++) {
+    const int chan0 = nt * (BN / 2) + (wn * (J / 2) + jb) * 32;
 #pragma unroll
-    for (int i2 = 0; i2 < 2; i2++)
+    for (int h = 0; h < 2; h++) {
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int r = i2 * 32 + acc32_row(lane, v);
-        const float gv = acc[2 * h + i2][0][v], uv = acc[2 * h + i2][1][v];
-        mid[r * kMidLdsStride + (lane & 31)] = silu(gv) * uv;
+      for (int i2 = 0; i2 < 2; i2++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int r = i2 * 32 + acc32_row(lane, v);
+          const float gv = acc[2 * h + i2][jb][v], uv = acc[2 * h + i2][J / 2 + jb][v];
+          mid[r * kMidLdsStride + (lane & 31)] = silu(gv) * uv;
+        }
+      __syncthreads();
+      const int row = m0 + wm * 128 + h * 64 + lane;
+      float v[32];
+      uint32_t amax = 0;
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        v[j] = mid[lane * kMidLdsStride + j];
+        amax = max(amax, abs_bits(v[j]));
       }
-    __syncthreads();
-    const int row = m0 + wm * 128 + h * 64 + lane;
-    float v[32];
-    uint32_t amax = 0;
-#pragma unroll
-    for (int j = 0; j < 32; j++) {
-      v[j] = mid[lane * kMidLdsStride + j];
-      amax = max(amax, abs_bits(v[j]));
+      const uint32_t sb = mxfp4_scale_byte(amax);
+      uint4 o = make_uint4(0, 0, 0, 0);
+      if (sb != 255u) {
+        o.x = fp4x8_from_f32(v + 0, sb);
+        o.y = fp4x8_from_f32(v + 8, sb);
+        o.z = fp4x8_from_f32(v + 16, sb);
+        o.w = fp4x8_from_f32(v + 24, sb);
+      }
+      if (row < M) {
+        *reinterpret_cast<uint4*>(mp + (size_t)row * mid_row_bytes + chan0 / 2) = o;
+        g.cs[(size_t)row * mid_row_blocks + chan0 / 32] = (uint8_t)sb;
+      }
+      __syncthreads();
     }
-    const uint32_t sb = mxfp4_scale_byte(amax);
-    uint4 o = make_uint4(0, 0, 0, 0);
-    if (sb != 255u) {
-      o.x = fp4x8_from_f32(v + 0, sb);
-      o.y = fp4x8_from_f32(v + 8, sb);
-      o.z = fp4x8_from_f32(v + 16, sb);
-      o.w = fp4x8_from_f32(v + 24, sb);
-    }
-    if (row < M) {
-      *reinterpret_cast<uint4*>(mp + (size_t)row * mid_row_bytes + chan0 / 2) = o;
-      g.cs[(size_t)row * mid_row_blocks + chan0 / 32] = (uint8_t)sb;
-    }
-    __syncthreads();
   }
+}
+
+template <bool DUAL, int BN>
+static hipError_t launch_bn(const Fp4GemmArgs& g, hipStream_t st) {
+  constexpr int kStage = (kAFrag + BN / 32 * 2) * 1024;
+  const int MT = (g.m + kFBM - 1) / kFBM;
+  const int NT = DUAL ? g.n / (BN / 2) : g.n / BN;
+  const int lds_mid = 4 * 64 * kMidLdsStride * 4;  // reuses the tile buffers
+  const int lds = 2 * kStage > lds_mid ? 2 * kStage : lds_mid;
+  hipLaunchKernelGGL((k_gemm_fp4<DUAL, BN>), dim3(MT * NT), dim3(256), lds, st, g);
+  return hipGetLastError();
 }
 
 // Preconditions (caller): k % 128 == 0; DUAL: n % 64 == 0; else n % 128 == 0.
 hipError_t launch_gemm_fp4(int dual, const Fp4GemmArgs& g, hipStream_t st) {
-  const int MT = (g.m + kFBM - 1) / kFBM;
-  const int NT = dual ? g.n / (kFBN / 2) : g.n / kFBN;
-  const int lds_tiles = 2 * kStageBytes;           // 48 KB
-  const int lds_mid = 4 * 64 * kMidLdsStride * 4;  // 33 KB, reuses the tiles
-  if (dual) {
-    const int lds = lds_tiles > lds_mid ? lds_tiles : lds_mid;
-    hipLaunchKernelGGL(k_gemm_fp4<true>, dim3(MT * NT), dim3(256), lds, st, g);
-  } else {
-    hipLaunchKernelGGL(k_gemm_fp4<false>, dim3(MT * NT), dim3(256), lds_tiles, st, g);
-  }
-  return hipGetLastError();
+  if (dual) return launch_bn<true, 128>(g, st);
+  return launch_bn<false, 128>(g, st);
 }
 
 }  // namespace mx

@@ -117,57 +117,42 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
   uint4 areg[ACH];
   BChunk<BKIND> breg[NB];
 
-  auto load_a = [&](int kb) {
-#pragma unroll
-    for (int c = 0; c < ACH; c++) {
-      const int idx = tid + c * 256;
-      if (A_F32) {
-        const int r = idx >> 3, q = idx & 7;  // 8 chunks of 4 floats per row
-        const int row = m0 + r;
-        if (row < M)
-          areg[c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(g.a) +
-                                                    (size_t)row * K + kb * 32 + q * 4);
-        else
-          areg[c] = make_uint4(0, 0, 0, 0);
-      } else {
-        const int r = idx >> 2, q = idx & 3;  // 4 chunks of 8 halves per row
-        const int row = m0 + r;
-        if (row < M)
-          areg[c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(g.a) +
-                                                    (size_t)row * K + kb * 32 + q * 8);
-        else
-          areg[c] = make_uint4(0, 0, 0, 0);
-      }
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < ACH; c++) {
-      const int idx = tid + c * 256;
-      if (A_F32) {
-        const int r = idx >> 3, q = idx & 7;
-        v4h h;
-        h[0] = (_Float16)__builtin_bit_cast(float, areg[c].x);
-        h[1] = (_Float16)__builtin_bit_cast(float, areg[c].y);
-        h[2] = (_Float16)__builtin_bit_cast(float, areg[c].z);
-        h[3] = (_Float16)__builtin_bit_cast(float, areg[c].w);
-        *reinterpret_cast<v4h*>(&As[buf][r * kLdsRow + q * 4]) = h;
-      } else {
-        const int r = idx >> 2, q = idx & 3;
-        *reinterpret_cast<uint4*>(&As[buf][r * kLdsRow + q * 8]) = areg[c];
-      }
-    }
-  };
-  auto load_b_all = [&](int kb) {
-    load_b<BKIND>(g.b0, g.s0, n0, kb, K, tid, breg[0]);
-    if (NB == 2) load_b<BKIND>(g.b1, g.s1, n0, kb, K, tid, breg[NB - 1]);
-  };
-  auto store_b = [&](int buf) {
-    const int r = tid >> 2, q = tid & 3;
-#pragma unroll
-    for (int j = 0; j < NB; j++)
-      *reinterpret_cast<uint4*>(&Bs[buf][(j * kBN + r) * kLdsRow + q * 8]) = decode_b<BKIND>(breg[j]);
-  };
+#define MX_LOAD_A(kb)                                                                      \
+  _Pragma("unroll") for (int c = 0; c < ACH; c++) {                                        \
+    const int idx = tid + c * 256;                                                         \
+    /* rows past M re-read row M-1: unconditional loads, and those tile rows */            \
+    /* only feed output rows that are never stored */                                      \
+    if (A_F32) {                                                                           \
+      const int row = min(m0 + (idx >> 3), M - 1);                                         \
+      areg[c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(g.a) +      \
+                                                (size_t)row * K + (kb) * 32 + (idx & 7) * 4); \
+    } else {                                                                               \
+      const int row = min(m0 + (idx >> 2), M - 1);                                         \
+      areg[c] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(g.a) +   \
+                                                (size_t)row * K + (kb) * 32 + (idx & 3) * 8); \
+    }                                                                                      \
+  }
+#define MX_STORE_A(buf)                                                                    \
+  _Pragma("unroll") for (int c = 0; c < ACH; c++) {                                        \
+    const int idx = tid + c * 256;                                                         \
+    if (A_F32) {                                                                           \
+      v4h h;                                                                               \
+      h[0] = (_Float16)__builtin_bit_cast(float, areg[c].x);                               \
+      h[1] = (_Float16)__builtin_bit_cast(float, areg[c].y);                               \
+      h[2] = (_Float16)__builtin_bit_cast(float, areg[c].z);                               \
+      h[3] = (_Float16)__builtin_bit_cast(float, areg[c].w);                               \
+      *reinterpret_cast<v4h*>(&As[buf][(idx >> 3) * kLdsRow + (idx & 7) * 4]) = h;         \
+    } else {                                                                               \
+      *reinterpret_cast<uint4*>(&As[buf][(idx >> 2) * kLdsRow + (idx & 3) * 8]) = areg[c]; \
+    }                                                                                      \
+  }
+#define MX_LOAD_B(kb)                                                                      \
+  load_b<BKIND>(g.b0, g.s0, n0, (kb), K, tid, breg[0]);                                   \
+  if (NB == 2) load_b<BKIND>(g.b1, g.s1, n0, (kb), K, tid, breg[NB - 1]);
+#define MX_STORE_B(buf)                                                                    \
+  _Pragma("unroll") for (int j = 0; j < NB; j++)                                           \
+    *reinterpret_cast<uint4*>(&Bs[buf][(j * kBN + (tid >> 2)) * kLdsRow + (tid & 3) * 8]) = \
+        decode_b<BKIND>(breg[j]);
 
   v16f acc[NB][MB];
 #pragma unroll
@@ -177,19 +162,20 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; v++) acc[j][i][v] = 0.0f;
 
-  load_a(0);
-  load_b_all(0);
-  store_a(0);
-  store_b(0);
+  MX_LOAD_A(0)
+  MX_LOAD_B(0)
+  MX_STORE_A(0)
+  MX_STORE_B(0)
   __syncthreads();
 
   const int frag_row = lane & 31, frag_k = (lane >> 5) * 8;
   for (int kt = 0; kt < KT; kt++) {
     const int buf = kt & 1;
-    if (kt + 1 < KT) {
-      load_a(kt + 1);
-      load_b_all(kt + 1);
-    }
+    // Prefetch the next step unconditionally (the last step re-reads itself
+    // into the idle buffer) so no load sits behind a branch.
+    const int kn = kt + 1 < KT ? kt + 1 : kt;
+    MX_LOAD_A(kn)
+    MX_LOAD_B(kn)
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       v8h af[MB], bf[NB];
@@ -206,10 +192,8 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < MB; i++) acc[j][i] = mfma_f16_32x32x16(af[i], bf[j], acc[j][i]);
     }
-    if (kt + 1 < KT) {
-      store_a(buf ^ 1);
-      store_b(buf ^ 1);
-    }
+    MX_STORE_A(buf ^ 1)
+    MX_STORE_B(buf ^ 1)
     __syncthreads();
   }
 
@@ -246,6 +230,11 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
     }
   }
 }
+
+#undef MX_LOAD_A
+#undef MX_STORE_A
+#undef MX_LOAD_B
+#undef MX_STORE_B
 
 template <int BKIND, int EPI, int A_F32>
 static hipError_t launch_bm(const GemmArgs& g, hipStream_t st) {

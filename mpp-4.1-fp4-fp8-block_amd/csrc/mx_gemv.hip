@@ -1,163 +1,210 @@
-// mx_gemv.hip - decode-shaped (tokens <= 16) MXFP4 GEMV with split-K.
+// mx_gemv.hip - decode-shaped (tokens <= 16) MXFP4 GEMV.
 //
 // The reference runs every shape through the same 64 x NT matmul2d tile
 // (MXFP4Kernels.metal:138-173) and only for tokens % 64 == 0
-// (main.swift:946).  On MI355X a 1..16-token MLP is bound by HBM: the whole
-// job is streaming 4-bit weights once.  This kernel is built for that:
+// (main.swift:946).  On MI355X a 1..16-token MLP is bound by HBM and by the
+// fixed cost of a launch: the whole job is streaming 4-bit weights once, so
+// this kernel is shaped for that.
 //
-//   unit  = one wave64 = 16 weight rows x (K / splits) of the reduction
-//   lane  = (row n = lane % 16, block group g = lane / 16); per 128-K step
-//           it loads 16 contiguous bytes of its row (one whole 32-element
-//           E8M0 block) plus that block's scale byte, decodes them with
-//           v_cvt_scalef32_pk_f16_fp4 and feeds v_mfma_f32_16x16x32_f16
-//           (tokens padded to 16 rows; the MFMA is never the bottleneck).
-//           The activations use the same K permutation, so each lane reads
-//           64 contiguous bytes of x per step (L2-resident).
-//   split = partial sums go to a workspace; the last wave of a row group
-//           (atomic counter, self-resetting) adds the partials in split
-//           order - deterministic - and applies the epilogue:
-//             single: out = f16(sum)
-//             dual:   mid = f16(silu(sum_gate) * sum_up)   (swiglu_float)
+//   workgroup = 16 weight rows x the whole K; its W waves split K between
+//               them (wave w takes 128-K steps w, w+W, ...), so at any time
+//               the workgroup sweeps one contiguous stretch of each row.
+//               For the gate/up pass the 16 rows are 8 gate channels and the
+//               same 8 up channels, so silu(g)*u is formed in the workgroup.
+//   lane      = (row r = lane % 16, block group g = lane / 16); per step it
+//               loads 16 contiguous bytes of its row (one whole 32-element
+//               E8M0 block), decodes them with v_cvt_scalef32_pk_f16_fp4 and
+//               feeds v_mfma_f32_16x16x32_f16 (tokens padded to 16 rows; the
+//               MFMA is never the bottleneck).  The activations follow the
+//               same K permutation.
+//   order     = every weight load of the wave is issued first (scheduling
+//               barriers keep the order, so the compiler's waits release the
+//               steps one by one); while they are in flight the workgroup
+//               stages the activations and its rows' E8M0 scales in LDS with
+//               coalesced loads, so the per-step operand reads are ds_reads.
+//   reduction = the W partial 16x16 tiles are added in LDS in wave order
+//               (deterministic), then the epilogue writes f16:
+//                 single: out[t][n] = sum
+//                 dual:   mid[t][c] = silu(sum_gate) * sum_up  (swiglu_float)
 //
-// Loads are issued four K steps at a time per lane (64-128 B in flight per
-// lane) so that each CU keeps tens of KB of HBM requests outstanding.
+// Measured on MI355X: a one-shot launch of this size is dominated by fixed
+// costs (an empty kernel costs ~2.5 us back to back, a pure 14.7 MB read
+// ~4 us); cross-workgroup synchronisation is far worse (an agent-scope grid
+// barrier costs ~14 us), so gate/up and down stay two plain launches.
 #include "mx_device.h"
 #include "mx_internal.h"
 
 namespace mx {
 
-constexpr int kGroupRows = 16;
 constexpr int kStepK = 128;   // K per lane step: 4 lane groups x 32-element blocks
-constexpr int kBatch = 4;     // steps whose loads are issued together
+// NSTEP: steps per wave whose weight loads are issued together (2, 4 or 8).
+constexpr int kW = 8;         // waves per workgroup
 
-template <bool DUAL>
-__global__ __launch_bounds__(256) void k_gemv_mxfp4(GemvArgs g) {
-  const int lane = threadIdx.x & 63;
-  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int groups = g.n / kGroupRows;
-  if (unit >= groups * g.splits) return;
-  const int grp = unit % groups, split = unit / groups;
-  const int n = grp * kGroupRows + (lane & 15);
-  const int lg = lane >> 4;                    // block within the 128-K step
-  const int tok = lane & 15;                   // activation row this lane feeds
+// Dynamic LDS layout: [scales 16 rows x K/32 bytes][x T rows x (K+8) halves]
+// [reduction W x 16 x 17 floats].
+__host__ __device__ inline size_t gemv_lds_bytes(int t, int k) {
+  const size_t s = (size_t)16 * (k / 32);
+  const size_t xs = (size_t)t * (k + 8) * 2;
+  return ((s + 15) / 16) * 16 + ((xs + 15) / 16) * 16 + (size_t)kW * 16 * 17 * 4;
+}
+
+template <bool DUAL, int NSTEP>
+__global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, lg = lane >> 4;
   const int K = g.k, T = g.t;
-  const int steps = K / kStepK / g.splits;
-  const int step0 = split * steps;
-  const size_t row_bytes = (size_t)K / 2, row_blocks = (size_t)K / 32;
+  const int S = K / kStepK;
+  const int KB = K / 32;
+  uint8_t* s_lds = lds;
+  uint16_t* x_lds = reinterpret_cast<uint16_t*>(lds + (((size_t)16 * KB + 15) / 16) * 16);
+  float* red = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(x_lds) +
+                                        (((size_t)T * (K + 8) * 2 + 15) / 16) * 16);
 
-  const uint8_t* w0 = g.b0 + (size_t)n * row_bytes + lg * 16;
-  const uint8_t* sc0 = g.s0 + (size_t)n * row_blocks + lg;
-  const uint8_t* w1 = DUAL ? g.b1 + (size_t)n * row_bytes + lg * 16 : nullptr;
-  const uint8_t* sc1 = DUAL ? g.s1 + (size_t)n * row_blocks + lg : nullptr;
-  const bool has_tok = tok < T;
-  const uint16_t* xr = g.x + (size_t)(has_tok ? tok : 0) * K + lg * 32;
+  // Weight / scale row of tile row `rr`.
+  auto row_ptrs = [&](int rr, const uint8_t*& w, const uint8_t*& s) {
+    if (DUAL) {
+      const int c = blockIdx.x * 8 + (rr & 7);
+      w = (rr < 8 ? g.b0 : g.b1) + (size_t)c * (K / 2);
+      s = (rr < 8 ? g.s0 : g.s1) + (size_t)c * KB;
+    } else {
+      const int n = blockIdx.x * 16 + rr;
+      w = g.b0 + (size_t)n * (K / 2);
+      s = g.s0 + (size_t)n * KB;
+    }
+  };
+  const uint8_t* wrow;
+  const uint8_t* srow;
+  row_ptrs(r, wrow, srow);
+  wrow += lg * 16;
 
+  // 1) Issue this wave's first batch of weight loads.
+  uint4 wv[NSTEP];
+#pragma unroll
+  for (int b = 0; b < NSTEP; b++) {
+    const int st = min(wave + b * kW, S - 1);  // tail steps re-read a valid step
+    const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
+    wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // 2) While they are in flight, stage x [T][K] and the 16 rows' scales.
+  for (int i = tid; i < T * (K / 8); i += 64 * kW) {
+    const int t = i / (K / 8), c = i % (K / 8);
+    *reinterpret_cast<uint4*>(x_lds + (size_t)t * (K + 8) + c * 8) =
+        *reinterpret_cast<const uint4*>(g.x + (size_t)t * K + c * 8);
+  }
+  for (int i = tid; i < 16 * (KB / 4); i += 64 * kW) {
+    const int rr = i / (KB / 4), c = i % (KB / 4);
+    const uint8_t* w;
+    const uint8_t* s;
+    row_ptrs(rr, w, s);
+    *reinterpret_cast<uint32_t*>(s_lds + (size_t)rr * KB + c * 4) =
+        *reinterpret_cast<const uint32_t*>(s + c * 4);
+  }
+  __syncthreads();
+
+  // Lane r feeds activation row r; rows >= T re-read row T-1 (their MFMA rows
+  // are never stored), so no load or read is predicated.
+  const uint16_t* xr = x_lds + (size_t)(r < T ? r : T - 1) * (K + 8) + lg * 32;
+  const uint8_t* sr = s_lds + (size_t)r * KB + lg;
   v4f acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
-  for (int s0 = 0; s0 < steps; s0 += kBatch) {
-    uint4 wv0[kBatch], wv1[kBatch];
-    uint32_t sb0[kBatch], sb1[kBatch];
-    uint4 xv[kBatch][4];
+  for (int s0 = wave; s0 < S; s0 += kW * NSTEP) {
+    if (s0 != wave) {  // later batches (K > 8 steps per wave): load them now
 #pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-      const int st = step0 + s0 + b;
-      if (s0 + b < steps) {
-        wv0[b] = *reinterpret_cast<const uint4*>(w0 + (size_t)st * 64);
-        sb0[b] = sc0[(size_t)st * 4];
-        if (DUAL) {
-          wv1[b] = *reinterpret_cast<const uint4*>(w1 + (size_t)st * 64);
-          sb1[b] = sc1[(size_t)st * 4];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-          xv[b][q] = has_tok ? *reinterpret_cast<const uint4*>(xr + (size_t)st * kStepK + q * 8)
-                             : make_uint4(0, 0, 0, 0);
+      for (int b = 0; b < NSTEP; b++) {
+        const int st = min(s0 + b * kW, S - 1);
+        const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
+        wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    // LDS operands are read one step ahead of their MFMAs so that LDS
+    // latency overlaps the previous step's decode and MFMAs.
+    uint4 xn[4];
+    uint32_t sn;
+    {
+      const int st = min(s0, S - 1);
 #pragma unroll
-    for (int b = 0; b < kBatch; b++) {
-      if (s0 + b < steps) {
-        const uint32_t wd0[4] = {wv0[b].x, wv0[b].y, wv0[b].z, wv0[b].w};
-        uint32_t wd1[4];
-        if (DUAL) {
-          wd1[0] = wv1[b].x; wd1[1] = wv1[b].y; wd1[2] = wv1[b].z; wd1[3] = wv1[b].w;
-        }
+      for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)st * kStepK + q * 8);
+      sn = sr[(size_t)st * 4];
+    }
+#pragma unroll
+    for (int b = 0; b < NSTEP; b++) {
+      const int st = s0 + b * kW;
+      uint4 xq[4] = {xn[0], xn[1], xn[2], xn[3]};
+      const uint32_t sbyte = sn;
+      if (b + 1 < NSTEP) {
+        const int stn = min(st + kW, S - 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)stn * kStepK + q * 8);
+        sn = sr[(size_t)stn * 4];
+      }
+      if (st < S) {  // wave-uniform; no global loads inside
+        const bool any255 = __ballot(sbyte == 255u) != 0;
+        const uint32_t wd[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const v8h a = __builtin_bit_cast(v8h, xv[b][q]);
-          acc0 = mfma_f16_16x16x32(a, fp4x8_dequant_f16(wd0[q], sb0[b]), acc0);
-          if (DUAL) acc1 = mfma_f16_16x16x32(a, fp4x8_dequant_f16(wd1[q], sb1[b]), acc1);
+          const v8h bq = fp4x8_dequant_f16_u(wd[q], sbyte, any255);
+          if (q & 1) acc1 = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq[q]), bq, acc1);
+          else acc0 = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq[q]), bq, acc0);
         }
       }
     }
   }
-  // acc element v: token row (lane/16)*4 + v, weight row n.
-  const int col_stride = DUAL ? 2 * g.n : g.n;
-  if (g.splits == 1) {
+
+  // acc element v: token (lane/16)*4 + v, column (weight row) lane % 16.
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const int t = (lane >> 4) * 4 + v;
-      if (t >= T) continue;
-      float r;
-      if (DUAL) r = silu(acc0[v]) * acc1[v];
-      else r = acc0[v];
-      g.out[(size_t)t * g.n + n] = f32_to_f16_bits(r);
+  for (int v = 0; v < 4; v++) red[(wave * 16 + lg * 4 + v) * 17 + r] = acc0[v] + acc1[v];
+  __syncthreads();
+  const int tt = tid >> 4, cc = tid & 15;
+  float tot = 0.0f;
+  if (tid < 256) {
+#pragma unroll
+    for (int w = 0; w < kW; w++) tot += red[(w * 16 + tt) * 17 + cc];
+  }
+  __syncthreads();
+  if (tid < 256) red[tt * 17 + cc] = tot;
+  __syncthreads();
+  if (DUAL) {
+    if (tid < 128) {
+      const int t = tid >> 3, j = tid & 7;
+      if (t < T) {
+        const float gv = red[t * 17 + j], uv = red[t * 17 + 8 + j];
+        g.out[(size_t)t * g.n + blockIdx.x * 8 + j] = f32_to_f16_bits(silu(gv) * uv);
+      }
     }
-    return;
+  } else {
+    if (tid < 256 && tt < T) g.out[(size_t)tt * g.n + blockIdx.x * 16 + cc] = f32_to_f16_bits(red[tt * 17 + cc]);
   }
-  float* part = g.partial + (size_t)split * T * col_stride;
-#pragma unroll
-  for (int v = 0; v < 4; v++) {
-    const int t = (lane >> 4) * 4 + v;
-    if (t >= T) continue;
-    part[(size_t)t * col_stride + n] = acc0[v];
-    if (DUAL) part[(size_t)t * col_stride + g.n + n] = acc1[v];
-  }
-  __threadfence();
-  uint32_t prev = 0;
-  if (lane == 0) prev = atomicAdd(&g.counters[grp], 1u);
-  prev = __shfl(prev, 0);
-  if (prev != (uint32_t)(g.splits - 1)) return;
-  __threadfence();
-#pragma unroll
-  for (int v = 0; v < 4; v++) {
-    const int t = (lane >> 4) * 4 + v;
-    if (t >= T) continue;
-    float s0 = 0.0f, s1 = 0.0f;
-    for (int s = 0; s < g.splits; s++) {
-      const float* p = g.partial + (size_t)s * T * col_stride + (size_t)t * col_stride;
-      s0 += p[n];
-      if (DUAL) s1 += p[g.n + n];
-    }
-    float r = DUAL ? silu(s0) * s1 : s0;
-    g.out[(size_t)t * g.n + n] = f32_to_f16_bits(r);
-  }
-  if (lane == 0) atomicExch(&g.counters[grp], 0u);
 }
 
-// Splits: as many as keep ~8 waves per CU busy while dividing the K steps.
-int gemv_pick_splits(int n, int k, int dual) {
-  (void)dual;
-  const int groups = n / kGroupRows;
-  const int steps = k / kStepK;
-  const int target = (2048 + groups - 1) / groups;
-  int best = 1;
-  for (int s = 1; s <= steps && s <= 64; s++)
-    if (steps % s == 0 && s <= target) best = s;
-  return best;
-}
-
-size_t gemv_partial_floats(int t, int n, int splits, int dual) {
-  return (size_t)splits * t * n * (dual ? 2 : 1);
-}
-
-// Preconditions (caller): 1 <= t <= 16, n % 16 == 0, k % 128 == 0,
-// (k/128) % splits == 0; counters zeroed once before first use.
-hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
-  const int units = (g.n / kGroupRows) * g.splits;
-  dim3 grid((units + 3) / 4);
-  if (dual) hipLaunchKernelGGL(k_gemv_mxfp4<true>, grid, dim3(256), 0, st, g);
-  else hipLaunchKernelGGL(k_gemv_mxfp4<false>, grid, dim3(256), 0, st, g);
+template <bool DUAL, int NSTEP>
+static hipError_t launch_ns(const GemvArgs& g, size_t lds, hipStream_t st) {
+  static bool attr_set = false;  // allow up to 160 KB of dynamic LDS (once per instance)
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4<DUAL, NSTEP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int groups = DUAL ? g.n / 8 : g.n / 16;
+  hipLaunchKernelGGL((k_gemv_mxfp4<DUAL, NSTEP>), dim3(groups), dim3(64 * kW), lds, st, g);
   return hipGetLastError();
 }
+
+// Preconditions (caller): 1 <= t <= 16, n % 16 == 0, k % 128 == 0 and
+// gemv_lds_bytes(t, k) <= 160 KB (checked here).  The batch size is the
+// number of K steps each wave owns (capped at 8), so no wave issues
+// redundant loads when K is short.
+hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
+  const size_t lds = gemv_lds_bytes(g.t, g.k);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const int per_wave = (g.k / kStepK + kW - 1) / kW;
+  if (per_wave <= 2) return dual ? launch_ns<true, 2>(g, lds, st) : launch_ns<false, 2>(g, lds, st);
+  if (per_wave <= 4) return dual ? launch_ns<true, 4>(g, lds, st) : launch_ns<false, 4>(g, lds, st);
+  return dual ? launch_ns<true, 8>(g, lds, st) : launch_ns<false, 8>(g, lds, st);
+}
+
+size_t gemv_lds_need(int t, int k) { return gemv_lds_bytes(t, k); }
 
 }  // namespace mx

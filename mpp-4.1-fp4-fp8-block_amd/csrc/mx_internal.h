@@ -57,19 +57,17 @@ struct GemmArgs {
 
 hipError_t launch_gemm_h(int bkind, int epi, const GemmArgs& g, hipStream_t st);
 
-// Decode-shaped (tokens <= 16) split-K GEMV family (mx_gemv.hip).
+// Decode-shaped (tokens <= 16) GEMV (mx_gemv.hip): one workgroup per 16
+// weight rows, K split across its waves and reduced in LDS.
 struct GemvArgs {
   const uint16_t* x;                      // f16 [T][K]
   const uint8_t* b0; const uint8_t* s0;   // MXFP4 weights (matrix 0)
   const uint8_t* b1; const uint8_t* s1;   // second matrix (dual / SwiGLU)
   uint16_t* out;                          // f16 [T][N] (out or mid)
-  float* partial;                         // [splits][T][N * nb] workspace
-  uint32_t* counters;                     // [N/16] zero-initialised, self-resetting
-  int t, n, k, splits;
+  int t, n, k;
 };
 hipError_t launch_gemv_mxfp4(int dual_swiglu, const GemvArgs& g, hipStream_t st);
-int gemv_pick_splits(int n, int k, int dual);
-size_t gemv_partial_floats(int t, int n, int splits, int dual);
+size_t gemv_lds_need(int t, int k);  // dynamic LDS of one workgroup (<= 160 KB to run)
 
 // W4A4 FP4 x FP4 scaled-MFMA GEMM (mx_gemm_fp4.hip).
 struct Fp4GemmArgs {

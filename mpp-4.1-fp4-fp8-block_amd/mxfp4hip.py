@@ -91,12 +91,12 @@ def load() -> ctypes.CDLL:
         "mx_swiglu": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int]),
         "mx_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp, _int,
-                                    _int, P(ctypes.c_double), P(ctypes.c_double), P(_int)]),
+                                    _int, _int, P(ctypes.c_double), P(ctypes.c_double), P(_int)]),
         "mx_mlp_kernel_name": (ctypes.c_char_p, [_int, _int, _int]),
         "mx_fmt_quantize": (_int, [_vp, _int, _vp, _int, _int, _vp, _vp]),
         "mx_fmt_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_fmt_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp,
-                                        _int, _int, P(ctypes.c_double)]),
+                                        _int, _int, _int, P(ctypes.c_double)]),
         "mx_fill_normal": (_int, [_vp, _vp, _int, _sz, _u64, _f, _f]),
         "mx_lcg_bytes": (None, [_u32, _sz, _vp]),
         "mx_lcg_pattern": (None, [_u32, _sz, _vp, _int, _vp]),
@@ -252,7 +252,7 @@ class Device:
                                           ctypes.byref(w), out.p))
 
     def mlp_benchmark(self, variant, tokens, hidden, inter, x: DevBuf, sets, out: DevBuf,
-                      warmup=1, iterations=20, per_kernel=True):
+                      warmup=1, iterations=20, per_kernel=True, graph=True):
         cfg = MlpConfig(tokens, hidden, inter)
         arr = (MlpWeights * len(sets))(*sets)
         secs = ctypes.c_double()
@@ -260,7 +260,7 @@ class Device:
         nk = ctypes.c_int(0)
         self._check(load().mx_mlp_benchmark(
             self.ctx, variant, ctypes.byref(cfg), x.p, arr, len(sets), out.p, warmup, iterations,
-            ctypes.byref(secs), kus if per_kernel else None,
+            1 if graph else 0, ctypes.byref(secs), kus if per_kernel else None,
             ctypes.byref(nk) if per_kernel else None))
         names = [load().mx_mlp_kernel_name(variant, tokens, i).decode() for i in range(nk.value)]
         return secs.value, dict(zip(names, list(kus)[:nk.value]))
@@ -275,13 +275,13 @@ class Device:
                                               ctypes.byref(w), out.p))
 
     def fmt_mlp_benchmark(self, wfmt, tokens, hidden, inter, x: DevBuf, sets, out: DevBuf,
-                          warmup=1, iterations=20):
+                          warmup=1, iterations=20, graph=True):
         cfg = MlpConfig(tokens, hidden, inter)
         arr = (MlpWeights * len(sets))(*sets)
         secs = ctypes.c_double()
         self._check(load().mx_fmt_mlp_benchmark(self.ctx, wfmt, ctypes.byref(cfg), x.p, arr,
                                                 len(sets), out.p, warmup, iterations,
-                                                ctypes.byref(secs)))
+                                                1 if graph else 0, ctypes.byref(secs)))
         return secs.value
 
 
