@@ -105,6 +105,7 @@ bool gemv_ok(const mx_mlp_config* cfg) {
 // Scratch layout for one variant; returns bytes needed.
 struct MlpScratch {
   size_t mid = 0, gate = 0, up = 0, wg = 0, wu = 0, wd = 0, xq = 0, xs = 0, mq = 0, ms = 0;
+  size_t sg = 0, su = 0, sd = 0;  // stage-major weight scale copies (W4A4)
   size_t total = 0;
 };
 
@@ -124,9 +125,19 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
     s.mid = take(T * I * 4);
   } else if (variant == MX_MLP_W4A4) {
     s.xq = take(T * H / 2);
-    s.xs = take(T * H / 32);
     s.mq = take(T * I / 2);
-    s.ms = take(T * I / 32);
+    if (mx::w4a4_stage_major_ok((int)H, (int)I)) {
+      // stage-major planes: [K/128][rows rounded up to 256] dwords
+      const size_t Tp = mx::stage_major_rows(T);
+      s.xs = take(Tp * H / 32);
+      s.ms = take(Tp * I / 32);
+      s.sg = take(I * H / 32);
+      s.su = take(I * H / 32);
+      s.sd = take(H * I / 32);
+    } else {
+      s.xs = take(T * H / 32);
+      s.ms = take(T * I / 32);
+    }
   }
   s.total = off;
   return s;
@@ -195,11 +206,26 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
     uint8_t* xs = ws + s.xs;
     uint8_t* mq = ws + s.mq;
     uint8_t* ms = ws + s.ms;
-    mx::Fp4GemmArgs gu{xq, xs, wg, sg, wu, su, mq, ms, T, I, H};
-    mx::Fp4GemmArgs dn{mq, ms, wd, sd, nullptr, nullptr, out, nullptr, T, H, I};
-    steps.push_back({"quantize_x_mxfp4", [=] { return mx::launch_mxfp4_quantize(x, MX_DTYPE_F16, xq, xs, T, H, st); }});
-    steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
-    steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});
+    if (mx::w4a4_stage_major_ok(H, I)) {
+      // One prologue launch quantizes x and re-lays the three weight scale
+      // planes stage-major; both GEMMs then fetch a stage's scales as one
+      // contiguous block.
+      uint8_t* sg2 = ws + s.sg;
+      uint8_t* su2 = ws + s.su;
+      uint8_t* sd2 = ws + s.sd;
+      mx::W4A4Prologue pro{static_cast<const uint16_t*>(x), xq, xs, sg, su, sd, sg2, su2, sd2, T, H, I};
+      mx::Fp4GemmArgs gu{xq, xs, wg, sg2, wu, su2, mq, ms, T, I, H, 1};
+      mx::Fp4GemmArgs dn{mq, ms, wd, sd2, nullptr, nullptr, out, nullptr, T, H, I, 1};
+      steps.push_back({"w4a4_prologue", [=] { return mx::launch_w4a4_prologue(pro, st); }});
+      steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
+      steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});
+    } else {
+      mx::Fp4GemmArgs gu{xq, xs, wg, sg, wu, su, mq, ms, T, I, H, 0};
+      mx::Fp4GemmArgs dn{mq, ms, wd, sd, nullptr, nullptr, out, nullptr, T, H, I, 0};
+      steps.push_back({"w4a4_prologue", [=] { return mx::launch_mxfp4_quantize(x, MX_DTYPE_F16, xq, xs, T, H, st); }});
+      steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
+      steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});
+    }
   }
   return MX_OK;
 }
@@ -461,7 +487,7 @@ const char* mx_mlp_kernel_name(int variant, int tokens, int index) {
   static const char* ref[] = {"gemm_h_mxfp4_gate_up_swiglu_half", "gemm_h_mxfp4_down_f32"};
   static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
                               "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
-  static const char* w4[] = {"quantize_x_mxfp4", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down"};
+  static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down"};
   if (index < 0) return nullptr;
   switch (variant) {
     case MX_MLP_FUSED: return index < 2 ? (tokens <= 16 ? fused_gemv[index] : fused[index]) : nullptr;

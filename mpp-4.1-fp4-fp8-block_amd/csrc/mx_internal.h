@@ -70,14 +70,35 @@ hipError_t launch_gemv_mxfp4(int dual_swiglu, const GemvArgs& g, hipStream_t st)
 size_t gemv_lds_need(int t, int k);  // dynamic LDS of one workgroup (<= 160 KB to run)
 
 // W4A4 FP4 x FP4 scaled-MFMA GEMM (mx_gemm_fp4.hip).
+// Scale planes come in two layouts:
+//   reference    [rows][K/32] bytes (GUIDE:48-50)
+//   stage-major  [K/128][rows_pad] dwords: the 4 E8M0 bytes of one 128-K
+//                stage of a row in one dword, all rows of a stage contiguous
+//                (rows_pad = rows rounded up to 256), so a 256-row tile's
+//                scales for one stage are one contiguous 1 KB.
 struct Fp4GemmArgs {
-  const uint8_t* a; const uint8_t* as;    // activations MXFP4 [M][K/2], [M][K/32]
-  const uint8_t* b0; const uint8_t* s0;   // weights MXFP4 [N][K/2], [N][K/32]
+  const uint8_t* a; const uint8_t* as;    // activations MXFP4 [M][K/2] + scales
+  const uint8_t* b0; const uint8_t* s0;   // weights MXFP4 [N][K/2] + scales
   const uint8_t* b1; const uint8_t* s1;   // up weights (dual epilogue)
   void* c;                                // f16 [M][N] or mid MXFP4 [M][N/2]
-  uint8_t* cs;                            // mid scales [M][N/32] (dual epilogue)
+  uint8_t* cs;                            // mid scales (dual epilogue)
   int m, n, k;
+  int stage_major;                        // 1: all scale planes stage-major
 };
 hipError_t launch_gemm_fp4(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+// 256x256-tile kernel for stage-major scales (mx_gemm_fp4_v3.hip).
+hipError_t launch_gemm_fp4_v3(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+// True when the stage-major 256x256 kernel takes this MLP (T x H x I).
+bool w4a4_stage_major_ok(int hidden, int inter);
+__host__ __device__ inline size_t stage_major_rows(size_t rows) { return (rows + 255) / 256 * 256; }
+// W4A4 prologue, one launch: x f16 [T][H] -> MXFP4 [T][H/2] + stage-major
+// scales, and the three weight scale planes -> stage-major copies.
+struct W4A4Prologue {
+  const uint16_t* x; uint8_t* xq; uint8_t* xs;
+  const uint8_t* sg; const uint8_t* su; const uint8_t* sd;   // reference layout
+  uint8_t* sg2; uint8_t* su2; uint8_t* sd2;                  // stage-major
+  int t, h, i;
+};
+hipError_t launch_w4a4_prologue(const W4A4Prologue& p, hipStream_t st);
 
 }  // namespace mx
