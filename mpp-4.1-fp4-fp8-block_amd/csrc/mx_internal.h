@@ -88,6 +88,12 @@ struct Fp4GemmArgs {
 hipError_t launch_gemm_fp4(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
 // 256x256-tile kernel for stage-major scales (mx_gemm_fp4_v3.hip).
 hipError_t launch_gemm_fp4_v3(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+// Same with a 4-slot LDS ring (mx_gemm_fp4_v4.hip), for K % 512 == 0.
+hipError_t launch_gemm_fp4_v4(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+bool gemm_fp4_v4_ok(int k);
+// Full-cache-line DMA, K stage 256 (mx_gemm_fp4_v5.hip), for K % 512 == 0.
+hipError_t launch_gemm_fp4_v5(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+bool gemm_fp4_v5_ok(int k);
 // True when the stage-major 256x256 kernel takes this MLP (T x H x I).
 bool w4a4_stage_major_ok(int hidden, int inter);
 __host__ __device__ inline size_t stage_major_rows(size_t rows) { return (rows + 255) / 256 * 256; }
