@@ -192,7 +192,7 @@ def main():
             r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
             sec[f"c2_{tag}"] = r
         for wfmt, tag in ((M.WFMT_FP8_E4M3, "fp8_e4m3"), (M.WFMT_FP8_E5M2, "fp8_e5m2"),
-                          (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32")):
+                          (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32"), (M.WFMT_W8A8, "w8a8")):
             r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, 2, 40, 4, seed=7,
                               wfmt=wfmt)
             wb = 3 * 4096 * 14336 * (0.5 if wfmt == M.WFMT_INT4 else 1)

@@ -148,6 +148,10 @@ int mx_mxfp4_matmul(mx_ctx* ctx, const void* a, int a_dtype, const uint8_t* b, v
  * mpp_mlp_f_h_f_n128 (a f32) (MPPMLPKernels.metal:39-48, 164-173). */
 int mx_gemm_f16(mx_ctx* ctx, const void* a, int a_dtype, const void* b, float* c, int m, int n,
                 int k);
+/* C i32 = A * B^T with A int8 [m][k], B int8 [n][k], exact i32 sums:
+ * mpp_mlp_i8_i8_i32_n128 (MPPMLPKernels.metal:61-70), the W8A8 core.
+ * n % 64 == 0, k % 128 == 0. */
+int mx_gemm_i8(mx_ctx* ctx, const int8_t* a, const int8_t* b, int32_t* c, int m, int n, int k);
 /* SwiGLU: variant 0 mpp_mlp_swiglu_float, 1 mpp_mlp_swiglu_half,
  * 2 mpp_mlp_swiglu_half_from_half, 3 mpp_mlp_swiglu_i8
  * (MPPMLPKernels.metal:186-257; ABI gate, up, mid, config). */

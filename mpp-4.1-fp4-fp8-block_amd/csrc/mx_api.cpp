@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <functional>
 #include <string>
 #include <vector>
@@ -106,6 +107,7 @@ bool gemv_ok(const mx_mlp_config* cfg) {
 struct MlpScratch {
   size_t mid = 0, gate = 0, up = 0, wg = 0, wu = 0, wd = 0, xq = 0, xs = 0, mq = 0, ms = 0;
   size_t sg = 0, su = 0, sd = 0;  // stage-major weight scale copies (W4A4)
+  size_t qws = 0;                 // split-K partials of the small-M GEMMs
   size_t total = 0;
 };
 
@@ -116,6 +118,9 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
   if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
     s.mid = take(T * I * 2);
+    const int e = variant == MX_MLP_REFROW ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16;
+    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, e, (int)T, (int)I, (int)H),
+                          mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_STORE_F32, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_DEQUANT) {
     s.wg = take(I * H * 2);
     s.wu = take(I * H * 2);
@@ -123,6 +128,8 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
     s.gate = take(T * I * 4);
     s.up = take(T * I * 4);
     s.mid = take(T * I * 4);
+    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_STORE_F32, (int)T, (int)I, (int)H),
+                          mx::gemm_q_ws_bytes(mx::AK_F32, mx::EPI_STORE_F16, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_W4A4) {
     s.xq = take(T * H / 2);
     s.mq = take(T * I / 2);
@@ -178,12 +185,15 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
   } else if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
     uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
     const bool ref = variant == MX_MLP_REFROW;
-    mx::GemmArgs gu{x, MX_DTYPE_F16, wg, sg, wu, su, mid, T, I, H};
-    mx::GemmArgs dn{mid, MX_DTYPE_F16, wd, sd, nullptr, nullptr, out, T, H, I};
-    steps.push_back({ref ? "gemm_h_mxfp4_gate_up_swiglu_half" : "gemm_h_mxfp4_gate_up_swiglu",
-                     [=] { return mx::launch_gemm_h(mx::BK_MXFP4, ref ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16, gu, st); }});
-    steps.push_back({ref ? "gemm_h_mxfp4_down_f32" : "gemm_h_mxfp4_down",
-                     [=] { return mx::launch_gemm_h(mx::BK_MXFP4, ref ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16, dn, st); }});
+    const int e_gu = ref ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16;
+    const int e_dn = ref ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
+    void* qws = ws + s.qws;
+    mx::QGemmArgs gu{x, nullptr, wg, sg, wu, su, mid, qws, T, I, H, 0};
+    mx::QGemmArgs dn{mid, nullptr, wd, sd, nullptr, nullptr, out, qws, T, H, I, 0};
+    steps.push_back({ref ? "gemm_q_mxfp4_gate_up_swiglu_half" : "gemm_q_mxfp4_gate_up_swiglu",
+                     [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_MXFP4, e_gu, gu, st); }});
+    steps.push_back({ref ? "gemm_q_mxfp4_down_f32" : "gemm_q_mxfp4_down",
+                     [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_MXFP4, e_dn, dn, st); }});
   } else if (variant == MX_MLP_DEQUANT) {
     uint16_t* wg16 = reinterpret_cast<uint16_t*>(ws + s.wg);
     uint16_t* wu16 = reinterpret_cast<uint16_t*>(ws + s.wu);
@@ -194,13 +204,14 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
     steps.push_back({"dequant_gate", [=] { return mx::launch_mxfp4_dequant_f16(wg, sg, wg16, I, H, st); }});
     steps.push_back({"dequant_up", [=] { return mx::launch_mxfp4_dequant_f16(wu, su, wu16, I, H, st); }});
     steps.push_back({"dequant_down", [=] { return mx::launch_mxfp4_dequant_f16(wd, sd, wd16, H, I, st); }});
-    mx::GemmArgs gg{x, MX_DTYPE_F16, wg16, nullptr, nullptr, nullptr, gate, T, I, H};
-    mx::GemmArgs gp{x, MX_DTYPE_F16, wu16, nullptr, nullptr, nullptr, up, T, I, H};
-    mx::GemmArgs dn{mid, MX_DTYPE_F32, wd16, nullptr, nullptr, nullptr, out, T, H, I};
-    steps.push_back({"gemm_h_h_f_gate", [=] { return mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F32, gg, st); }});
-    steps.push_back({"gemm_h_h_f_up", [=] { return mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F32, gp, st); }});
+    void* qws = ws + s.qws;
+    mx::QGemmArgs gg{x, nullptr, wg16, nullptr, nullptr, nullptr, gate, qws, T, I, H, 0};
+    mx::QGemmArgs gp{x, nullptr, wu16, nullptr, nullptr, nullptr, up, qws, T, I, H, 0};
+    mx::QGemmArgs dn{mid, nullptr, wd16, nullptr, nullptr, nullptr, out, qws, T, H, I, 0};
+    steps.push_back({"gemm_h_h_f_gate", [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, gg, st); }});
+    steps.push_back({"gemm_h_h_f_up", [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, gp, st); }});
     steps.push_back({"swiglu_float", [=] { return mx::launch_swiglu(0, gate, up, mid, (size_t)T * I, st); }});
-    steps.push_back({"gemm_f_h_down", [=] { return mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F16, dn, st); }});
+    steps.push_back({"gemm_f_h_down", [=] { return mx::launch_gemm_q(mx::AK_F32, mx::BK_F16, mx::EPI_STORE_F16, dn, st); }});
   } else {  // W4A4
     uint8_t* xq = ws + s.xq;
     uint8_t* xs = ws + s.xs;
@@ -437,6 +448,23 @@ static int check_gemm(mx_ctx* c, int m, int n, int k, const void* a, const void*
   return MX_OK;
 }
 
+// One GEMM through the small-M family when the shape fits it (k % 64),
+// else through the K-step-32 kernel.
+static int run_gemm(mx_ctx* c, const void* a, int a_dtype, int bk, const void* b, const void* scales,
+                    void* out, int epi, int m, int n, int k) {
+  const int ak = a_dtype == MX_DTYPE_F32 ? mx::AK_F32 : mx::AK_F16;
+  if (mx::gemm_q_ok(ak, bk, epi, m, n, k)) {
+    const size_t wsb = mx::gemm_q_ws_bytes(ak, epi, m, n, k);
+    if (int rc = ensure_ws(c, wsb)) return rc;
+    mx::QGemmArgs g{a, nullptr, b, scales, nullptr, nullptr, out, wsb ? c->ws : nullptr, m, n, k, 0};
+    MX_HIP(c, mx::launch_gemm_q(ak, bk, epi, g, c->stream));
+    return MX_OK;
+  }
+  mx::GemmArgs g{a, a_dtype, b, scales, nullptr, nullptr, out, m, n, k};
+  MX_HIP(c, mx::launch_gemm_h(bk, epi, g, c->stream));
+  return MX_OK;
+}
+
 int mx_mxfp4_matmul(mx_ctx* c, const void* a, int a_dtype, const uint8_t* b, void* out, int c_dtype,
                     int m, int n, int k, const uint8_t* scales) {
   if (!c) return MX_EINVAL;
@@ -446,10 +474,8 @@ int mx_mxfp4_matmul(mx_ctx* c, const void* a, int a_dtype, const uint8_t* b, voi
     return set_err(c, MX_EINVAL, "matmul A must be f16 or f32.");
   if (c_dtype != MX_DTYPE_F32 && c_dtype != MX_DTYPE_F16)
     return set_err(c, MX_EINVAL, "matmul C must be f32 or f16.");
-  mx::GemmArgs g{a, a_dtype, b, scales, nullptr, nullptr, out, m, n, k};
-  MX_HIP(c, mx::launch_gemm_h(mx::BK_MXFP4, c_dtype == MX_DTYPE_F32 ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16,
-                              g, c->stream));
-  return MX_OK;
+  const int epi = c_dtype == MX_DTYPE_F32 ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
+  return run_gemm(c, a, a_dtype, mx::BK_MXFP4, b, scales, out, epi, m, n, k);
 }
 
 int mx_gemm_f16(mx_ctx* c, const void* a, int a_dtype, const void* b, float* out, int m, int n, int k) {
@@ -457,8 +483,18 @@ int mx_gemm_f16(mx_ctx* c, const void* a, int a_dtype, const void* b, float* out
   if (int rc = check_gemm(c, m, n, k, a, b, out)) return rc;
   if (a_dtype != MX_DTYPE_F16 && a_dtype != MX_DTYPE_F32)
     return set_err(c, MX_EINVAL, "gemm A must be f16 or f32.");
-  mx::GemmArgs g{a, a_dtype, b, nullptr, nullptr, nullptr, out, m, n, k};
-  MX_HIP(c, mx::launch_gemm_h(mx::BK_F16, mx::EPI_STORE_F32, g, c->stream));
+  return run_gemm(c, a, a_dtype, mx::BK_F16, b, nullptr, out, mx::EPI_STORE_F32, m, n, k);
+}
+
+int mx_gemm_i8(mx_ctx* c, const int8_t* a, const int8_t* b, int32_t* out, int m, int n, int k) {
+  if (!c) return MX_EINVAL;
+  if (int rc = check_gemm(c, m, n, k, a, b, out)) return rc;
+  if (!mx::gemm_q_ok(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_I32, m, n, k))
+    return set_err(c, MX_EINVAL, "int8 matmul needs n %% 64 == 0 and k %% 128 == 0.");
+  const size_t wsb = mx::gemm_q_ws_bytes(mx::AK_I8, mx::EPI_STORE_I32, m, n, k);
+  if (int rc = ensure_ws(c, wsb)) return rc;
+  mx::QGemmArgs g{a, nullptr, b, nullptr, nullptr, nullptr, out, wsb ? c->ws : nullptr, m, n, k, 0};
+  MX_HIP(c, mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_I32, g, c->stream));
   return MX_OK;
 }
 
@@ -483,8 +519,8 @@ int mx_mlp_forward(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void*
 
 const char* mx_mlp_kernel_name(int variant, int tokens, int index) {
   static const char* fused_gemv[] = {"gemv_mxfp4_gate_up_swiglu", "gemv_mxfp4_down"};
-  static const char* fused[] = {"gemm_h_mxfp4_gate_up_swiglu", "gemm_h_mxfp4_down"};
-  static const char* ref[] = {"gemm_h_mxfp4_gate_up_swiglu_half", "gemm_h_mxfp4_down_f32"};
+  static const char* fused[] = {"gemm_q_mxfp4_gate_up_swiglu", "gemm_q_mxfp4_down"};
+  static const char* ref[] = {"gemm_q_mxfp4_gate_up_swiglu_half", "gemm_q_mxfp4_down_f32"};
   static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
                               "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
   static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down"};
@@ -632,21 +668,52 @@ static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const 
     case MX_WFMT_FP8_E5M2: bk = mx::BK_E5M2; break;
     case MX_WFMT_INT8: bk = mx::BK_INT8; break;
     case MX_WFMT_INT4: bk = mx::BK_INT4G32; break;
-    case MX_WFMT_W8A8: return set_err(c, MX_EINVAL, "W8A8 MLP is not available in this build.");
+    case MX_WFMT_W8A8: bk = mx::BK_I8; break;
     default: return set_err(c, MX_EINVAL, "Unknown weight format %d.", wfmt);
   }
   const mx_qmatrix* mats[3] = {&w->gate, &w->up, &w->down};
   for (const mx_qmatrix* m : mats)
-    if (!m->data || !m->scales || !aligned16(m->data))
+    if (!m->data || !m->scales || !aligned16(m->data) || (reinterpret_cast<uintptr_t>(m->scales) & 3u))
       return set_err(c, MX_EINVAL, "format weight buffers must be non-null and 16-byte aligned.");
   const int T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
-  if (int rc = ensure_ws(c, align_up((size_t)T * I * 2, 256))) return rc;
-  uint16_t* mid = static_cast<uint16_t*>(c->ws);
   hipStream_t st = c->stream;
-  mx::GemmArgs gu{x, MX_DTYPE_F16, w->gate.data, w->gate.scales, w->up.data, w->up.scales, mid, T, I, H};
-  mx::GemmArgs dn{mid, MX_DTYPE_F16, w->down.data, w->down.scales, nullptr, nullptr, out, T, H, I};
-  steps.push_back({"gemm_h_fmt_gate_up_swiglu", [=] { return mx::launch_gemm_h(bk, mx::EPI_SWIGLU_F16, gu, st); }});
-  steps.push_back({"gemm_h_fmt_down", [=] { return mx::launch_gemm_h(bk, mx::EPI_STORE_F16, dn, st); }});
+  if (bk == mx::BK_I8) {
+    // W8A8 (MPPMLPKernels.metal:61-70, 240-257 with BASELINE's scales):
+    // x -> int8 per token, i32 GEMMs, f32 mid re-quantized per token.
+    if (H % 128 || I % 128)
+      return set_err(c, MX_EINVAL, "W8A8 needs hidden and intermediate to be multiples of 128.");
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
+    const size_t o_xq = take((size_t)T * H), o_xs = take((size_t)T * 4), o_mid = take((size_t)T * I * 4),
+                 o_mq = take((size_t)T * I), o_ms = take((size_t)T * 4),
+                 o_qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_I8, mx::EPI_SWIGLU_F32, T, I, H),
+                                       mx::gemm_q_ws_bytes(mx::AK_I8, mx::EPI_STORE_F16, T, H, I)));
+    if (int rc = ensure_ws(c, off)) return rc;
+    uint8_t* ws = static_cast<uint8_t*>(c->ws);
+    int8_t* xq = reinterpret_cast<int8_t*>(ws + o_xq);
+    float* xs = reinterpret_cast<float*>(ws + o_xs);
+    float* mid = reinterpret_cast<float*>(ws + o_mid);
+    int8_t* mq = reinterpret_cast<int8_t*>(ws + o_mq);
+    float* ms = reinterpret_cast<float*>(ws + o_ms);
+    void* qws = ws + o_qws;
+    mx::QGemmArgs gu{xq, xs, w->gate.data, w->gate.scales, w->up.data, w->up.scales, mid, qws, T, I, H, 0};
+    mx::QGemmArgs dn{mq, ms, w->down.data, w->down.scales, nullptr, nullptr, out, qws, T, H, I, 0};
+    steps.push_back({"quant_x_int8", [=] { return mx::launch_quant_act_int8(x, MX_DTYPE_F16, T, H, xq, xs, st); }});
+    steps.push_back({"gemm_q_w8a8_gate_up_swiglu", [=] { return mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_SWIGLU_F32, gu, st); }});
+    steps.push_back({"quant_mid_int8", [=] { return mx::launch_quant_act_int8(mid, MX_DTYPE_F32, T, I, mq, ms, st); }});
+    steps.push_back({"gemm_q_w8a8_down", [=] { return mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_F16, dn, st); }});
+    return MX_OK;
+  }
+  const size_t mid_b = align_up((size_t)T * I * 2, 256);
+  const size_t qws_b = std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_SWIGLU_F16, T, I, H),
+                                mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_STORE_F16, T, H, I));
+  if (int rc = ensure_ws(c, mid_b + qws_b)) return rc;
+  uint16_t* mid = static_cast<uint16_t*>(c->ws);
+  void* qws = static_cast<uint8_t*>(c->ws) + mid_b;
+  mx::QGemmArgs gu{x, nullptr, w->gate.data, w->gate.scales, w->up.data, w->up.scales, mid, qws, T, I, H, 0};
+  mx::QGemmArgs dn{mid, nullptr, w->down.data, w->down.scales, nullptr, nullptr, out, qws, T, H, I, 0};
+  steps.push_back({"gemm_q_fmt_gate_up_swiglu", [=] { return mx::launch_gemm_q(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, gu, st); }});
+  steps.push_back({"gemm_q_fmt_down", [=] { return mx::launch_gemm_q(mx::AK_F16, bk, mx::EPI_STORE_F16, dn, st); }});
   return MX_OK;
 }
 

@@ -238,13 +238,21 @@ __global__ void k_swiglu(int variant, const void* __restrict__ gate, const void*
 // Weight-format quantizers.  One workgroup per row.
 // fmt 1 = FP8 E4M3 / 2 = FP8 E5M2 (scale amax/qmax), 3 = INT8 (amax/127).
 // Division in f32, matching the CPU oracle bit for bit.
-__global__ void k_quant_rowwise(int fmt, const float* __restrict__ w, int k,
+// Also the per-token INT8 activation quantizer of W8A8 (SRC_F16: x in f16).
+template <bool SRC_F16>
+__device__ __forceinline__ float ld_src(const void* p, size_t i) {
+  if (SRC_F16) return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  return reinterpret_cast<const float*>(p)[i];
+}
+
+template <bool SRC_F16>
+__global__ void k_quant_rowwise(int fmt, const void* __restrict__ w, int k,
                                 uint8_t* __restrict__ q, float* __restrict__ row_scale) {
   __shared__ float red[256];
   const int row = blockIdx.x;
-  const float* src = w + (size_t)row * k;
+  const size_t base = (size_t)row * k;
   float amax = 0.0f;
-  for (int i = threadIdx.x; i < k; i += blockDim.x) amax = fmaxf(amax, fabsf(src[i]));
+  for (int i = threadIdx.x; i < k; i += blockDim.x) amax = fmaxf(amax, fabsf(ld_src<SRC_F16>(w, base + i)));
   red[threadIdx.x] = amax;
   __syncthreads();
   for (int s = blockDim.x / 2; s > 0; s >>= 1) {
@@ -257,7 +265,8 @@ __global__ void k_quant_rowwise(int fmt, const float* __restrict__ w, int k,
   if (threadIdx.x == 0) row_scale[row] = sc;
   uint8_t* dst = q + (size_t)row * k;
   for (int i = threadIdx.x * 4; i < k; i += blockDim.x * 4) {
-    float v0 = src[i] / sc, v1 = src[i + 1] / sc, v2 = src[i + 2] / sc, v3 = src[i + 3] / sc;
+    const float v0 = ld_src<SRC_F16>(w, base + i) / sc, v1 = ld_src<SRC_F16>(w, base + i + 1) / sc,
+                v2 = ld_src<SRC_F16>(w, base + i + 2) / sc, v3 = ld_src<SRC_F16>(w, base + i + 3) / sc;
     uint32_t r;
     if (fmt == 1) r = fp8x4_from_f32<false>(v0, v1, v2, v3);
     else if (fmt == 2) r = fp8x4_from_f32<true>(v0, v1, v2, v3);
@@ -396,7 +405,21 @@ hipError_t launch_swiglu(int variant, const void* gate, const void* up, void* mi
 hipError_t launch_quant_rowwise(int fmt, const float* w, int rows, int k, uint8_t* q, float* scale,
                                 hipStream_t st) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quant_rowwise, dim3(rows), dim3(256), 0, st, fmt, w, k, q, scale);
+  hipLaunchKernelGGL(k_quant_rowwise<false>, dim3(rows), dim3(256), 0, st, fmt, w, k, q, scale);
+  return hipGetLastError();
+}
+
+// W8A8 activations: per-row INT8 with scale amax/127 (same arithmetic as
+// the weight rows, so one oracle function covers both).  k % 4 == 0.
+hipError_t launch_quant_act_int8(const void* x, int x_dtype, int rows, int k, int8_t* q,
+                                 float* scale, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  if (x_dtype == MX_DTYPE_F16)
+    hipLaunchKernelGGL(k_quant_rowwise<true>, dim3(rows), dim3(256), 0, st, 3, x, k,
+                       reinterpret_cast<uint8_t*>(q), scale);
+  else
+    hipLaunchKernelGGL(k_quant_rowwise<false>, dim3(rows), dim3(256), 0, st, 3, x, k,
+                       reinterpret_cast<uint8_t*>(q), scale);
   return hipGetLastError();
 }
 

@@ -1,0 +1,559 @@
+// mx_gemm_q.hip - GEMM family for small and medium token counts (BASELINE
+// configs 0, 2, 3 and the GEMM entry points): half / f32 / int8 activations
+// times quantized weights.
+//
+//   C[m][n] = sum_k A[m][k] * W[n][k]   (epilogue: store, SwiGLU, scales)
+//
+// Counterparts in the reference (root = Anemll/MPP-4.1-FP4-FP8-block):
+//   MXFP4 weights   mxfp4_native_sp_h_f_n64 / mxfp4_fused_h_f_n64
+//                   (MXFP4Kernels.metal:42-173, 264-286)
+//   f16 weights     mpp_mlp_h_h_f_n128 / mpp_mlp_f_h_f_n128 (MPPMLPKernels.metal:14-48, 164-173)
+//   FP8/INT8/INT4   mpp_mlp_h_fp8e4m3_f / _h_fp8e5m2_f / _h_i8_f / _h_i4_f
+//                   (MPPMLPKernels.metal:50-125), plus BASELINE's scales
+//   W8A8            mpp_mlp_i8_i8_i32_n128 (MPPMLPKernels.metal:61-70), i32
+//                   accumulation, per-token x scale and per-row weight scale
+//   SwiGLU          mpp_mlp_swiglu_float / _half (MPPMLPKernels.metal:186-220),
+//                   fused: a workgroup computes gate and up of the same channels
+//
+// Design (gfx950):
+//   tile      128 rows of A x 128 weight rows (SwiGLU: 64 gate + the same 64
+//             up channels), 4 wave64s in a 2 x 2 grid, each 64 x 64 = 2 x 2
+//             blocks of v_mfma_f32_32x32x16_f16 (W8A8: v_mfma_i32_32x32x32_i8).
+//             At most 80 KB of LDS and 64 accumulators, so two workgroups
+//             share a CU and hide each other's waits.
+//   K stage   64 (W8A8: 128).  A and B rows of a stage are moved global -> LDS
+//             by global_load_lds_dwordx4, whole rows per instruction (1 KB =
+//             8 rows of 128 B for f16), into a 2-slot ring of separate
+//             __shared__ arrays.  The 16-byte chunks of a row are XOR-swizzled
+//             (chunk c of row r at c ^ swz(r)) so the fragment reads
+//             (32 rows x one chunk) hit distinct banks; each DMA lane fetches
+//             the chunk that belongs in its LDS position.
+//   K order   within a stage, lane half h of a fragment owns the contiguous
+//             K range [32h, 32h+32) (W8A8 [64h, 64h+64)); both operands use
+//             the same order, so the dot products are unchanged and every
+//             lane reads whole 16-byte chunks.  A 4-bit weight lane therefore
+//             holds exactly one 32-element block: one E8M0 / f16 scale.
+//   decode    weights are widened in registers after the LDS read: FP4 with
+//             v_cvt_scalef32_pk_f16_fp4 (E8M0 applied), FP8 with
+//             v_cvt_scalef32_pk_f16_{fp8,bf8}, INT8 / INT4 with the 0x6400
+//             exponent trick, f32 activations with v_cvt_f16_f32.
+//   split K   shapes with few tiles split K over gridDim.y; the partial tiles
+//             (f32, or i32 for W8A8) are summed in split order by a second
+//             kernel that also runs the epilogue, so results are deterministic.
+#include <type_traits>
+
+#include "mx_device.h"
+#include "mx_internal.h"
+
+namespace mx {
+namespace qgemm {
+
+constexpr int kTM = 128;  // tile rows (A)
+
+template <int AK> struct AInfo;
+template <> struct AInfo<AK_F16> { static constexpr int KS = 64, RB = 128; };
+template <> struct AInfo<AK_F32> { static constexpr int KS = 64, RB = 256; };
+template <> struct AInfo<AK_I8> { static constexpr int KS = 128, RB = 128; };
+
+// bytes of one weight row per stage
+template <int BK> constexpr int b_row_bytes(int ks) {
+  return BK == BK_F16 ? ks * 2 : (BK == BK_MXFP4 || BK == BK_INT4G32) ? ks / 2 : ks;
+}
+
+// Chunk swizzle for rows of R bytes (C = R/16 chunks): rows that share a
+// 256-byte bank line get different chunk rotations.
+template <int R>
+__device__ __forceinline__ int swz(int row) {
+  constexpr int C = R / 16;
+  constexpr int RPL = 16 / C > 0 ? 16 / C : 1;  // rows per 256 bytes
+  return (row / RPL) % C;
+}
+
+// 16-byte global -> LDS DMA of one lane (the LDS base is wave-uniform).
+// Kept behind a device function: referenced directly from this kernel
+// template's body, the builtin stops the host pass from emitting the
+// kernel's launch stub.
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt(n) only.
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// INT8 x8 -> f16 x8 (exact): byte b -> half(1024 + (b ^ 0x80)) - 1152.
+__device__ __forceinline__ v8h i8x8_to_f16(uint32_t w0, uint32_t w1) {
+  const uint32_t x[2] = {w0 ^ 0x80808080u, w1 ^ 0x80808080u};
+  v8h out;
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x[t], 0x04010400u);  // b0, b1
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x[t], 0x04030402u);  // b2, b3
+    v2h l = __builtin_bit_cast(v2h, lo) - (v2h){(_Float16)1152.0f, (_Float16)1152.0f};
+    v2h h = __builtin_bit_cast(v2h, hi) - (v2h){(_Float16)1152.0f, (_Float16)1152.0f};
+    out[4 * t] = l[0]; out[4 * t + 1] = l[1]; out[4 * t + 2] = h[0]; out[4 * t + 3] = h[1];
+  }
+  return out;
+}
+
+// INT4 x8 (one dword, low nibble first) -> f16 x8: ((n ^ 8) - 8) * scale,
+// rounded once to f16 (PackedNumericKernels.metal:30-33).
+__device__ __forceinline__ v8h i4x8_to_f16(uint32_t w, _Float16 sc) {
+  const uint32_t x = w ^ 0x88888888u;
+  const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;  // even / odd nibbles
+  // halves: 1024 + nibble
+  const uint32_t p0 = 0x64006400u | (lo & 0xffu) | ((hi & 0xffu) << 16);
+  const uint32_t p1 = 0x64006400u | ((lo >> 8) & 0xffu) | (((hi >> 8) & 0xffu) << 16);
+  const uint32_t p2 = 0x64006400u | ((lo >> 16) & 0xffu) | (((hi >> 16) & 0xffu) << 16);
+  const uint32_t p3 = 0x64006400u | ((lo >> 24) & 0xffu) | (((hi >> 24) & 0xffu) << 16);
+  const v2h off = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const v2h s2 = {sc, sc};
+  v2h q0 = (__builtin_bit_cast(v2h, p0) - off) * s2;
+  v2h q1 = (__builtin_bit_cast(v2h, p1) - off) * s2;
+  v2h q2 = (__builtin_bit_cast(v2h, p2) - off) * s2;
+  v2h q3 = (__builtin_bit_cast(v2h, p3) - off) * s2;
+  v8h out;
+  out[0] = q0[0]; out[1] = q0[1]; out[2] = q1[0]; out[3] = q1[1];
+  out[4] = q2[0]; out[5] = q2[1]; out[6] = q3[0]; out[7] = q3[1];
+  return out;
+}
+
+template <int BK>
+__device__ __forceinline__ v8h fp8x8_to_f16(uint32_t w0, uint32_t w1) {
+  const uint32_t w[2] = {w0, w1};
+  v8h h;
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    v2h lo, hi;
+    if (BK == BK_E4M3) {
+      lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[t], 1.0f, false);
+      hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[t], 1.0f, true);
+    } else {
+      lo = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w[t], 1.0f, false);
+      hi = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w[t], 1.0f, true);
+    }
+    h[4 * t] = lo[0]; h[4 * t + 1] = lo[1]; h[4 * t + 2] = hi[0]; h[4 * t + 3] = hi[1];
+  }
+  return h;
+}
+
+// One output element's epilogue.  g (and u for SwiGLU) are the raw sums.
+template <int EPI>
+__device__ __forceinline__ void epi_store(void* c, size_t o, float x0, float u) {
+  if (EPI == EPI_STORE_F32 || EPI == EPI_STORE_I32) {
+    reinterpret_cast<float*>(c)[o] = x0;
+  } else if (EPI == EPI_STORE_F16) {
+    reinterpret_cast<uint16_t*>(c)[o] = f32_to_f16_bits(x0);
+  } else if (EPI == EPI_SWIGLU_F32) {
+    reinterpret_cast<float*>(c)[o] = (x0 / (1.0f + expf(-x0))) * u;
+  } else if (EPI == EPI_SWIGLU_F16) {
+    reinterpret_cast<uint16_t*>(c)[o] = f32_to_f16_bits((x0 / (1.0f + expf(-x0))) * u);
+  } else {  // EPI_SWIGLU_HALF: silu(clamp(g/16, +-20)) * u/16 (MPPMLPKernels.metal:204-220)
+    const float gg = fminf(fmaxf(x0 * 0.0625f, -20.0f), 20.0f);
+    reinterpret_cast<uint16_t*>(c)[o] = f32_to_f16_bits((gg / (1.0f + expf(-gg))) * (u * 0.0625f));
+  }
+}
+
+constexpr bool is_dual(int epi) {
+  return epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_HALF || epi == EPI_SWIGLU_F32;
+}
+constexpr bool row_scaled(int bk) { return bk == BK_E4M3 || bk == BK_E5M2 || bk == BK_INT8 || bk == BK_I8; }
+
+// Scale a raw sum: weight row scale, and the per-token scale for W8A8.
+template <int AK, int BK>
+__device__ __forceinline__ float scaled(float acc, const QGemmArgs& g, const float* ws, int row, int col) {
+  float v = acc;
+  if (AK == AK_I8) v = v * g.a_scale[row];
+  if (row_scaled(BK)) v = v * ws[col];
+  return v;
+}
+
+// NWB: 32-column weight blocks per wave (2: 128 weight rows per tile, 1: 64).
+template <int AK, int BK, int EPI, int NWB>
+__global__ __launch_bounds__(256, 2) void k_gemm_q(QGemmArgs g) {
+  constexpr bool DUAL = is_dual(EPI);
+  constexpr int KS = AInfo<AK>::KS;
+  constexpr int RA = AInfo<AK>::RB;          // A bytes per row per stage
+  constexpr int RB = b_row_bytes<BK>(KS);    // B bytes per row per stage
+  constexpr int TBR = NWB * 64;               // weight rows per tile
+  constexpr int NA = kTM * RA / 1024 / 4;    // A DMA instructions per wave per stage
+  constexpr int NBW = TBR * RB / 1024;       // B DMA instructions per stage (all waves)
+  constexpr int NB = NBW >= 4 ? NBW / 4 : 1; // per wave (waves >= NBW issue none)
+  constexpr bool SCALES4 = BK == BK_MXFP4 || BK == BK_INT4G32;
+  constexpr int KSTEPS = 4;
+  static_assert(NA >= 1 && (NBW >= 4 ? NBW % 4 == 0 : true), "tile / stage mismatch");
+  using AccT = typename std::conditional<AK == AK_I8, v16i, v16f>::type;
+
+  __shared__ __attribute__((aligned(16))) uint8_t a_s0[kTM * RA];
+  __shared__ __attribute__((aligned(16))) uint8_t a_s1[kTM * RA];
+  __shared__ __attribute__((aligned(16))) uint8_t b_s0[TBR * RB];
+  __shared__ __attribute__((aligned(16))) uint8_t b_s1[TBR * RB];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int M = g.m, K = g.k;
+  const int m0 = blockIdx.x % g.tiles_m * kTM;
+  const int nt = blockIdx.x / g.tiles_m;
+  const int n0 = DUAL ? nt * 64 : nt * TBR;  // first channel / weight row
+  const int KT = K / KS / (int)gridDim.y;     // stages of this split
+  const int kt0 = (int)blockIdx.y * KT;
+  const size_t a_row = (size_t)K * (AK == AK_F32 ? 4 : AK == AK_F16 ? 2 : 1);
+  const size_t b_row = (size_t)b_row_bytes<BK>(K);
+
+  // ---- DMA sources (per lane, per instruction)
+  constexpr int CA = RA / 16, CB = RB / 16;  // chunks per row
+  const uint8_t* a_src[NA];
+#pragma unroll
+  for (int q = 0; q < NA; q++) {
+    const int r = (wave * NA + q) * (1024 / RA) + lane / CA;  // tile row
+    const int c = (lane % CA) ^ swz<RA>(r);
+    a_src[q] = reinterpret_cast<const uint8_t*>(g.a) + (size_t)min(m0 + r, M - 1) * a_row + c * 16;
+  }
+  const uint8_t* b_src[NB];
+  const bool b_issuer = NBW >= 4 || wave < NBW;
+#pragma unroll
+  for (int q = 0; q < NB; q++) {
+    const int r = (NBW >= 4 ? wave * NB + q : min(wave, NBW - 1)) * (1024 / RB) + lane / CB;
+    const int c = (lane % CB) ^ swz<RB>(r);
+    const uint8_t* base;
+    int wrow;
+    if (DUAL) {
+      base = reinterpret_cast<const uint8_t*>(r < 64 ? g.b0 : g.b1);
+      wrow = n0 + (r & 63);
+    } else {
+      base = reinterpret_cast<const uint8_t*>(g.b0);
+      wrow = n0 + r;
+    }
+    b_src[q] = base + (size_t)wrow * b_row + c * 16;
+  }
+
+  // ---- fragment reads: lane (r32, h); A blocks i (rows 64wm + 32i), B
+  // blocks j (tile rows: dual -> gate / up rows 32wn.., else 64wn + 32j or 32wn).
+  const int r32 = lane & 31, h = lane >> 5;
+  int b_blk[NWB];
+#pragma unroll
+  for (int j = 0; j < NWB; j++) b_blk[j] = DUAL ? j * 64 + wn * 32 : (NWB == 2 ? wn * 64 + j * 32 : wn * 32);
+  // 4-bit scales: lane's block index within the stage is h (2 blocks / stage)
+  const uint8_t* sc_src[NWB];
+  if (SCALES4) {
+#pragma unroll
+    for (int j = 0; j < NWB; j++) {
+      const int tr = b_blk[j] + r32;
+      const int wrow = DUAL ? n0 + (tr & 63) : n0 + tr;
+      const uint8_t* sb = reinterpret_cast<const uint8_t*>(DUAL && tr >= 64 ? g.s1 : g.s0);
+      const int esz = BK == BK_INT4G32 ? 2 : 1;
+      sc_src[j] = sb + ((size_t)wrow * (K / 32) + (size_t)kt0 * (KS / 32) + h) * esz;
+    }
+  }
+
+  AccT acc[2][NWB];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < NWB; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
+
+  uint32_t scv[2][NWB];  // 4-bit scales of the stage in flight / in use
+
+#define MXQ_ISSUE(S, AS, BS, P)                                                                    \
+  {                                                                                                \
+    const size_t ka_ = (size_t)(kt0 + (S)) * RA, kb_ = (size_t)(kt0 + (S)) * RB;                   \
+    _Pragma("unroll") for (int q = 0; q < NA; q++)                                                 \
+      dma16(a_src[q] + ka_, (AS) + (wave * NA + q) * 1024);                                         \
+    if (b_issuer) {                                                                                \
+      _Pragma("unroll") for (int q = 0; q < NB; q++) {                                             \
+        const int qi_ = NBW >= 4 ? wave * NB + q : wave;                                           \
+        dma16(b_src[q] + kb_, (BS) + qi_ * 1024);                                                  \
+      }                                                                                            \
+    }                                                                                              \
+    if (SCALES4) {                                                                                 \
+      _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
+        const uint8_t* p_ = sc_src[j] + (size_t)(S) * (KS / 32) * (BK == BK_INT4G32 ? 2 : 1);     \
+        scv[P][j] = BK == BK_INT4G32 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_; \
+      }                                                                                            \
+    }                                                                                              \
+  }
+  // vmcnt that leaves exactly one stage (the one just issued) in flight
+  const int vm_stage = NA + (b_issuer ? NB : 0) + (SCALES4 ? NWB : 0);
+
+#define MXQ_WAIT_PREV()                                                                            \
+  {                                                                                                \
+    if (vm_stage == NA + NB + (SCALES4 ? NWB : 0)) __builtin_amdgcn_s_waitcnt(wait_vm(NA + NB + (SCALES4 ? NWB : 0))); \
+    else __builtin_amdgcn_s_waitcnt(wait_vm(NA + (SCALES4 ? NWB : 0)));                             \
+  }
+
+#define MXQ_COMPUTE(AS, BS, P)                                                                     \
+  {                                                                                                \
+    _Pragma("unroll") for (int s = 0; s < KSTEPS; s++) {                                           \
+      if (AK == AK_I8) {                                                                           \
+        v4i af[2], bf[NWB];                                                                         \
+        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                            \
+          const int r_ = wm * 64 + i * 32 + r32;                                                   \
+          af[i] = *reinterpret_cast<const v4i*>((AS) + r_ * RA + (((4 * h + s) ^ swz<RA>(r_)) << 4)); \
+        }                                                                                          \
+        _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                           \
+          const int r_ = b_blk[j] + r32;                                                           \
+          bf[j] = *reinterpret_cast<const v4i*>((BS) + r_ * RB + (((4 * h + s) ^ swz<RB>(r_)) << 4)); \
+        }                                                                                          \
+        _Pragma("unroll") for (int i = 0; i < 2; i++)                                              \
+          _Pragma("unroll") for (int j = 0; j < NWB; j++)                                           \
+            acc[i][j] = (AccT)__builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], (v16i)acc[i][j], 0, 0, 0); \
+      } else {                                                                                     \
+        v8h af[2], bf[NWB];                                                                         \
+        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                            \
+          const int r_ = wm * 64 + i * 32 + r32;                                                   \
+          if (AK == AK_F16) {                                                                      \
+            af[i] = *reinterpret_cast<const v8h*>((AS) + r_ * RA + (((4 * h + s) ^ swz<RA>(r_)) << 4)); \
+          } else {                                                                                 \
+            const v4f lo_ = *reinterpret_cast<const v4f*>((AS) + r_ * RA + (((8 * h + 2 * s) ^ swz<RA>(r_)) << 4)); \
+            const v4f hi_ = *reinterpret_cast<const v4f*>((AS) + r_ * RA + (((8 * h + 2 * s + 1) ^ swz<RA>(r_)) << 4)); \
+            _Pragma("unroll") for (int t = 0; t < 4; t++) {                                        \
+              af[i][t] = (_Float16)lo_[t];                                                         \
+              af[i][4 + t] = (_Float16)hi_[t];                                                     \
+            }                                                                                      \
+          }                                                                                        \
+        }                                                                                          \
+        _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                           \
+          const int r_ = b_blk[j] + r32;                                                           \
+          if (BK == BK_F16) {                                                                      \
+            bf[j] = *reinterpret_cast<const v8h*>((BS) + r_ * RB + (((4 * h + s) ^ swz<RB>(r_)) << 4)); \
+          } else if (BK == BK_MXFP4 || BK == BK_INT4G32) {                                         \
+            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RB + ((h ^ swz<RB>(r_)) << 4)); \
+            if (BK == BK_MXFP4) bf[j] = fp4x8_dequant_f16(w_[s], scv[P][j]);                       \
+            else bf[j] = i4x8_to_f16(w_[s], __builtin_bit_cast(_Float16, (uint16_t)scv[P][j]));    \
+          } else {                                                                                 \
+            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RB + (((2 * h + (s >> 1)) ^ swz<RB>(r_)) << 4)); \
+            const uint32_t w0_ = (s & 1) ? w_[2] : w_[0], w1_ = (s & 1) ? w_[3] : w_[1];          \
+            if (BK == BK_INT8) bf[j] = i8x8_to_f16(w0_, w1_);                                      \
+            else bf[j] = fp8x8_to_f16<BK>(w0_, w1_);                                               \
+          }                                                                                        \
+        }                                                                                          \
+        _Pragma("unroll") for (int i = 0; i < 2; i++)                                              \
+          _Pragma("unroll") for (int j = 0; j < NWB; j++)                                           \
+            acc[i][j] = (AccT)mfma_f16_32x32x16(af[i], bf[j], (v16f)acc[i][j]);                    \
+      }                                                                                            \
+    }                                                                                              \
+  }
+
+  // Pipeline: stage k+1's DMA is in flight while stage k is computed.
+  // Scheduling barriers keep each stage's DMA issue, wait and barrier in
+  // place: otherwise the compiler hoists the next stage's scale arithmetic
+  // above the partial wait and has to drain every load first.
+#define MXQ_SYNC_POINT()                                                                           \
+  __builtin_amdgcn_sched_barrier(0);                                                               \
+  MXQ_WAIT_PREV()                                                                                  \
+  __builtin_amdgcn_s_barrier();                                                                    \
+  __builtin_amdgcn_sched_barrier(0);
+  MXQ_ISSUE(0, a_s0, b_s0, 0)
+  int kt = 0;
+  for (; kt + 2 <= KT; kt += 2) {
+    MXQ_ISSUE(kt + 1, a_s1, b_s1, 1)
+    MXQ_SYNC_POINT()
+    MXQ_COMPUTE(a_s0, b_s0, 0)
+    __builtin_amdgcn_s_barrier();  // slot 0 free
+    MXQ_ISSUE(min(kt + 2, KT - 1), a_s0, b_s0, 0)
+    MXQ_SYNC_POINT()
+    MXQ_COMPUTE(a_s1, b_s1, 1)
+    __builtin_amdgcn_s_barrier();  // slot 1 free
+  }
+#undef MXQ_SYNC_POINT
+  if (kt < KT) {  // odd stage count: the last stage sits in slot 0
+    __builtin_amdgcn_s_waitcnt(wait_vm(0));
+    __builtin_amdgcn_s_barrier();
+    MXQ_COMPUTE(a_s0, b_s0, 0)
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+#undef MXQ_ISSUE
+#undef MXQ_WAIT_PREV
+#undef MXQ_COMPUTE
+
+  // ---- epilogue, or the raw partial tile when K is split (separate loops
+  // behind one uniform branch).
+  constexpr int PL = DUAL ? 2 : 1;
+  if (gridDim.y > 1) {
+    const size_t plane = (size_t)M * g.n;
+    uint32_t* w = reinterpret_cast<uint32_t*>(g.ws) + (size_t)blockIdx.y * PL * plane;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+#pragma unroll
+      for (int jj = 0; jj < (DUAL ? 1 : NWB); jj++) {
+        const int col = DUAL ? n0 + wn * 32 + r32 : n0 + b_blk[jj] + r32;
+        uint32_t gv[16], uv[16];
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          // copy the vector element to a scalar first: __builtin_bit_cast of
+          // a vector-element subscript yields element 0 for every v
+          const auto ge = acc[i][jj][v], ue = acc[i][1][v];
+          gv[v] = __builtin_bit_cast(uint32_t, ge);
+          uv[v] = DUAL ? __builtin_bit_cast(uint32_t, ue) : 0u;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, v);
+          if (row < M) {
+            const size_t o = (size_t)row * g.n + col;
+            w[o] = gv[v];
+            if (DUAL) w[plane + o] = uv[v];
+          }
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+#pragma unroll
+    for (int jj = 0; jj < (DUAL ? 1 : NWB); jj++) {
+      const int col = DUAL ? n0 + wn * 32 + r32 : n0 + b_blk[jj] + r32;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, v);
+        if (row >= M) continue;
+        const size_t o = (size_t)row * g.n + col;
+        if (EPI == EPI_STORE_I32) {
+          reinterpret_cast<int*>(g.c)[o] = (int)acc[i][jj][v];
+          continue;
+        }
+        const float g0 = AK == AK_I8 ? (float)(int)acc[i][jj][v] : (float)acc[i][jj][v];
+        const float x0 = scaled<AK, BK>(g0, g, reinterpret_cast<const float*>(g.s0), row, col);
+        float u = 0.0f;
+        if (DUAL) {
+          const float u0 = AK == AK_I8 ? (float)(int)acc[i][1][v] : (float)acc[i][1][v];
+          u = scaled<AK, BK>(u0, g, reinterpret_cast<const float*>(g.s1), row, col);
+        }
+        epi_store<EPI>(g.c, o, x0, u);
+      }
+    }
+  }
+}
+
+// Split-K reduction + epilogue: one thread per output element.
+template <int AK, int BK, int EPI>
+__global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
+  constexpr bool DUAL = is_dual(EPI);
+  constexpr int PL = DUAL ? 2 : 1;
+  const size_t plane = (size_t)g.m * g.n;
+  const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= plane) return;
+  const int row = (int)(o / g.n), col = (int)(o % g.n);
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(g.ws);
+  float sums[2];
+  if (EPI == EPI_STORE_I32) {
+    int s = 0;
+    for (int k = 0; k < splits; k++) s += (int)w[(size_t)k * plane + o];
+    reinterpret_cast<int*>(g.c)[o] = s;
+    return;
+  }
+#pragma unroll
+  for (int p = 0; p < PL; p++) {
+    if (AK == AK_I8) {
+      int s = 0;
+      for (int k = 0; k < splits; k++) s += (int)w[((size_t)k * PL + p) * plane + o];
+      sums[p] = (float)s;
+    } else {
+      float s = 0.0f;
+      for (int k = 0; k < splits; k++) s += __builtin_bit_cast(float, w[((size_t)k * PL + p) * plane + o]);
+      sums[p] = s;
+    }
+  }
+  const float x0 = scaled<AK, BK>(sums[0], g, reinterpret_cast<const float*>(g.s0), row, col);
+  const float u = DUAL ? scaled<AK, BK>(sums[PL - 1], g, reinterpret_cast<const float*>(g.s1), row, col) : 0.0f;
+  epi_store<EPI>(g.c, o, x0, u);
+}
+
+template <int AK, int BK, int EPI, int NWB>
+hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
+  QGemmArgs g = g0;
+  g.tiles_m = (g.m + kTM - 1) / kTM;
+  const int tiles_n = is_dual(EPI) ? g.n / 64 : g.n / (NWB * 64);
+  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g);
+  if (splits > 1) {
+    const size_t n = (size_t)g.m * g.n;
+    hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, splits);
+  }
+  return hipGetLastError();
+}
+
+template <int AK, int BK, int EPI>
+hipError_t launch_wn(const QGemmArgs& g, int splits, hipStream_t st) {
+  if (is_dual(EPI) || g.n % 128 == 0) return launch_q<AK, BK, EPI, 2>(g, splits, st);
+  return launch_q<AK, BK, EPI, 1>(g, splits, st);
+}
+
+int stage_k(int ak) { return ak == AK_I8 ? 128 : 64; }
+
+}  // namespace qgemm
+
+using namespace qgemm;
+
+// Split count: enough workgroups to cover the CUs twice when the tiles
+// alone do not, keeping at least 4 stages per split.
+int gemm_q_splits(int ak, int epi, int m, int n, int k) {
+  const int tiles = ((m + kTM - 1) / kTM) * (is_dual(epi) ? n / 64 : (n % 128 == 0 ? n / 128 : n / 64));
+  const int kt = k / stage_k(ak);
+  int s = 1;
+  while (tiles * s < 384 && kt % (2 * s) == 0 && kt / (2 * s) >= 4) s *= 2;
+  return s;
+}
+
+size_t gemm_q_ws_bytes(int ak, int epi, int m, int n, int k) {
+  const int s = gemm_q_splits(ak, epi, m, n, k);
+  return s > 1 ? (size_t)s * (is_dual(epi) ? 2 : 1) * m * n * 4 : 0;
+}
+
+bool gemm_q_ok(int ak, int bk, int epi, int m, int n, int k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % stage_k(ak)) return false;
+  if (n % 64) return false;
+  if (ak == AK_I8)
+    return bk == BK_I8 && (epi == EPI_SWIGLU_F32 || epi == EPI_STORE_F16 || epi == EPI_STORE_F32 || epi == EPI_STORE_I32);
+  return bk != BK_I8 && epi != EPI_STORE_I32 && epi != EPI_SWIGLU_F32;
+}
+
+#define MXQ_EPIS(AK, BK)                                                                            \
+  switch (epi) {                                                                                    \
+    case EPI_STORE_F32: return launch_wn<AK, BK, EPI_STORE_F32>(g, s, st);                          \
+    case EPI_STORE_F16: return launch_wn<AK, BK, EPI_STORE_F16>(g, s, st);                          \
+    case EPI_SWIGLU_F16: return launch_wn<AK, BK, EPI_SWIGLU_F16>(g, s, st);                        \
+    case EPI_SWIGLU_HALF: return launch_wn<AK, BK, EPI_SWIGLU_HALF>(g, s, st);                      \
+    default: return hipErrorInvalidValue;                                                           \
+  }
+
+hipError_t launch_gemm_q(int ak, int bk, int epi, const QGemmArgs& g, hipStream_t st) {
+  if (!gemm_q_ok(ak, bk, epi, g.m, g.n, g.k)) return hipErrorInvalidValue;
+  const int s = gemm_q_splits(ak, epi, g.m, g.n, g.k);
+  if (s > 1 && !g.ws) return hipErrorInvalidValue;
+  if (ak == AK_I8) {
+    switch (epi) {
+      case EPI_SWIGLU_F32: return launch_wn<AK_I8, BK_I8, EPI_SWIGLU_F32>(g, s, st);
+      case EPI_STORE_F16: return launch_wn<AK_I8, BK_I8, EPI_STORE_F16>(g, s, st);
+      case EPI_STORE_F32: return launch_wn<AK_I8, BK_I8, EPI_STORE_F32>(g, s, st);
+      case EPI_STORE_I32: return launch_wn<AK_I8, BK_I8, EPI_STORE_I32>(g, s, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (ak == AK_F32) {
+    if (epi != EPI_STORE_F32 && epi != EPI_STORE_F16) return hipErrorInvalidValue;
+    switch (bk) {
+      case BK_F16:
+        return epi == EPI_STORE_F32 ? launch_wn<AK_F32, BK_F16, EPI_STORE_F32>(g, s, st)
+                                    : launch_wn<AK_F32, BK_F16, EPI_STORE_F16>(g, s, st);
+      case BK_MXFP4:
+        return epi == EPI_STORE_F32 ? launch_wn<AK_F32, BK_MXFP4, EPI_STORE_F32>(g, s, st)
+                                    : launch_wn<AK_F32, BK_MXFP4, EPI_STORE_F16>(g, s, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch (bk) {
+    case BK_F16: MXQ_EPIS(AK_F16, BK_F16)
+    case BK_MXFP4: MXQ_EPIS(AK_F16, BK_MXFP4)
+    case BK_E4M3: MXQ_EPIS(AK_F16, BK_E4M3)
+    case BK_E5M2: MXQ_EPIS(AK_F16, BK_E5M2)
+    case BK_INT8: MXQ_EPIS(AK_F16, BK_INT8)
+    case BK_INT4G32: MXQ_EPIS(AK_F16, BK_INT4G32)
+  }
+  return hipErrorInvalidValue;
+}
+#undef MXQ_EPIS
+
+}  // namespace mx

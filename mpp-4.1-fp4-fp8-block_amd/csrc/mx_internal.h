@@ -37,6 +37,14 @@ enum BKind : int {
   BK_E5M2 = 3,     // FP8 E5M2 [N][K] + f32 row scale [N]
   BK_INT8 = 4,     // int8 [N][K] + f32 row scale [N]
   BK_INT4G32 = 5,  // int4 [N][K/2] + f16 scale [N][K/32]
+  BK_I8 = 6,       // int8 [N][K] + f32 row scale [N], int8 activations (W8A8)
+};
+
+// Activation encodings of the small-M GEMM family (mx_gemm_q.hip).
+enum AKind : int {
+  AK_F16 = 0,      // f16 [M][K]
+  AK_F32 = 1,      // f32 [M][K] (rounded to f16 for the MFMA)
+  AK_I8 = 2,       // int8 [M][K] + f32 per-row (token) scale [M]
 };
 
 // Epilogues.
@@ -45,6 +53,8 @@ enum Epi : int {
   EPI_STORE_F16 = 1,     // C f16 [M][N]
   EPI_SWIGLU_F16 = 2,    // dual B: mid f16 = silu(g) * u              (swiglu_float)
   EPI_SWIGLU_HALF = 3,   // dual B: mid f16 = silu(clamp(g/16)) * u/16  (swiglu_half)
+  EPI_SWIGLU_F32 = 4,    // dual B: mid f32 = silu(g) * u               (W8A8 mid)
+  EPI_STORE_I32 = 5,     // C i32 [M][N], raw integer sums (AK_I8 x BK_I8, no scales)
 };
 
 struct GemmArgs {
@@ -56,6 +66,23 @@ struct GemmArgs {
 };
 
 hipError_t launch_gemm_h(int bkind, int epi, const GemmArgs& g, hipStream_t st);
+
+// Small / medium-M GEMM family (mx_gemm_q.hip): 128 x 128 tiles, 64-K
+// stages (128 for W8A8), split K with an ordered reduction for few tiles.
+struct QGemmArgs {
+  const void* a;                          // activations (AKind)
+  const float* a_scale;                   // per-row scale for AK_I8
+  const void* b0; const void* s0;         // weights + scales (matrix 0)
+  const void* b1; const void* s1;         // second matrix for dual epilogues
+  void* c;                                // output
+  void* ws;                               // split-K partials (gemm_q_ws_bytes)
+  int m, n, k;                            // n = rows of each weight matrix
+  int tiles_m;                            // set by the launcher
+};
+bool gemm_q_ok(int akind, int bkind, int epi, int m, int n, int k);
+size_t gemm_q_ws_bytes(int akind, int epi, int m, int n, int k);
+int gemm_q_splits(int akind, int epi, int m, int n, int k);
+hipError_t launch_gemm_q(int akind, int bkind, int epi, const QGemmArgs& g, hipStream_t st);
 
 // Decode-shaped (tokens <= 16) GEMV (mx_gemv.hip): one workgroup per 16
 // weight rows, K split across its waves and reduced in LDS.

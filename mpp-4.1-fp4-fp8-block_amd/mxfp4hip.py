@@ -25,7 +25,7 @@ EXPORTS = [
     "mx_create", "mx_destroy", "mx_last_error", "mx_status_string", "mx_device_info",
     "mx_set_stream", "mx_get_stream", "mx_sync", "mx_alloc", "mx_free", "mx_upload",
     "mx_download", "mx_memset", "mx_roundtrip", "mx_pack", "mx_unpack", "mx_mxfp4_quantize",
-    "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_swiglu", "mx_mlp_forward",
+    "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_gemm_i8", "mx_swiglu", "mx_mlp_forward",
     "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_fmt_quantize", "mx_fmt_mlp_forward",
     "mx_fmt_mlp_benchmark", "mx_fill_normal", "mx_lcg_bytes", "mx_lcg_pattern", "mx_lcg_half",
     "mx_lcg_int8", "mx_checksum_f32", "mx_checksum_i32", "mx_checksum_f16raw",
@@ -88,6 +88,7 @@ def load() -> ctypes.CDLL:
         "mx_mxfp4_dequant_f16": (_int, [_vp, _vp, _vp, _vp, _int, _int]),
         "mx_mxfp4_matmul": (_int, [_vp, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp]),
         "mx_gemm_f16": (_int, [_vp, _vp, _int, _vp, _vp, _int, _int, _int]),
+        "mx_gemm_i8": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int]),
         "mx_swiglu": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int]),
         "mx_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp, _int,
@@ -232,6 +233,9 @@ class Device:
 
     def gemm_f16(self, a: DevBuf, a_dtype, b: DevBuf, c: DevBuf, m, n, k):
         self._check(load().mx_gemm_f16(self.ctx, a.p, a_dtype, b.p, c.p, m, n, k))
+
+    def gemm_i8(self, a: DevBuf, b: DevBuf, c: DevBuf, m, n, k):
+        self._check(load().mx_gemm_i8(self.ctx, a.p, b.p, c.p, m, n, k))
 
     def swiglu(self, variant, gate: DevBuf, up: DevBuf, mid: DevBuf, tokens, inter):
         self._check(load().mx_swiglu(self.ctx, variant, gate.p, up.p, mid.p, tokens, inter))

@@ -14,6 +14,33 @@ from mlp_data import MlpData, sample_rows
 
 pytestmark = pytest.mark.gpu
 FMTS = [M.WFMT_FP8_E4M3, M.WFMT_FP8_E5M2, M.WFMT_INT8, M.WFMT_INT4]
+MLP_FMTS = FMTS + [M.WFMT_W8A8]
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 128), (77, 192, 1024), (128, 256, 4096), (260, 128, 256)])
+def test_gemm_i8_bitexact(dev, m, n, k):
+    """The W8A8 core (mpp_mlp_i8_i8_i32_n128, MPPMLPKernels.metal:61-70):
+    exact int32 sums, including split K (128 x 256 x 4096) and ragged M."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    a[0, :] = -128   # extreme row: |sum| up to k * 2^14
+    b[0, :] = -128
+    da, db, dc = dev.upload(a), dev.upload(b), dev.alloc(m * n * 4)
+    dev.gemm_i8(da, db, dc, m, n, k)
+    got = dev.download(dc, np.int32, (m, n))
+    ref = a.astype(np.int64) @ b.astype(np.int64).T
+    assert np.array_equal(got.astype(np.int64), ref)
+    for buf in (da, db, dc):
+        buf.free()
+
+
+def test_gemm_i8_rejects_bad_shapes(dev):
+    a, b, c = dev.alloc(64 * 256), dev.alloc(64 * 256), dev.alloc(64 * 64 * 4)
+    for (m, n, k) in ((4, 64, 96), (4, 96, 128), (0, 64, 128)):
+        with pytest.raises(M.MxError) as e:
+            dev.gemm_i8(a, b, c, m, n, k)
+        assert e.value.code == M.MX_EINVAL
 
 
 @pytest.mark.parametrize("wfmt", FMTS)
@@ -51,7 +78,7 @@ def oracle_fmt(d, wfmt, rows=None):
     return O.mlp_format(wfmt, x, qg, sg, qu, su, qd, sd, d.H, d.I, rows=rows, threads=16)
 
 
-@pytest.mark.parametrize("wfmt", FMTS)
+@pytest.mark.parametrize("wfmt", MLP_FMTS)
 @pytest.mark.parametrize("T", [3, 128])
 def test_format_mlp_small(dev, wfmt, T):
     d = MlpData(dev, T, 512, 1024, seed=wfmt * 10 + T, wfmt=wfmt)
@@ -62,7 +89,7 @@ def test_format_mlp_small(dev, wfmt, T):
     d.free()
 
 
-@pytest.mark.parametrize("wfmt", FMTS)
+@pytest.mark.parametrize("wfmt", MLP_FMTS)
 def test_config3_formats(dev, wfmt):
     d = MlpData(dev, 128, 4096, 14336, seed=31 + wfmt, wfmt=wfmt)
     rows = sample_rows(128, 16)

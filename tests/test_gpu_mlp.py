@@ -27,8 +27,10 @@ def check(got, ref, tol=TOL, cos_min=COS, what=""):
     assert rel <= tol and cos >= cos_min, (what, rel, cos)
 
 
+# Shapes cover both tile widths (n % 128, n % 64), split K (few tiles, long
+# K), ragged M and the K-step-32 fallback kernel (k % 64 != 0).
 @pytest.mark.parametrize("m,n,k", [(1, 128, 256), (7, 192, 512), (64, 128, 1024), (100, 256, 512),
-                                   (300, 64, 2048)])
+                                   (300, 64, 2048), (5, 64, 96)])
 def test_mxfp4_matmul(dev, m, n, k):
     rng = np.random.default_rng(m + n + k)
     a = rng.standard_normal((m, k)).astype(np.float16)
