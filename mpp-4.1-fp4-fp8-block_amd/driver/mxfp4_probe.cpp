@@ -1,0 +1,366 @@
+// mxfp4_probe - command-line host driver over libmxfp4hip, the counterpart of
+// the reference's MetalFP41Probe executable (Sources/MetalFP41Probe/main.swift).
+// Swift is not available on this platform, so the driver is C++ on the C ABI.
+//
+// Same surface as the reference:
+//   (no flags)            packed numeric KAT probe: FP4 E2M1, FP8 E4M3, FP8 E5M2
+//                         roundtrips (main.swift:98-162), printed as
+//                         "[ok] <name>" / input / unpacked / expected / bytes
+//   --skip-tensor         skips the tensor-object probe (no counterpart on ROCm)
+//   --mlp-benchmark       gated MLP benchmark rows (runMLPBenchmark, :586-1521)
+//     --mlp-tokens=T --mlp-hidden=H --mlp-intermediate=I --mlp-iterations=N
+//     (defaults 128, 1024, 4*H, 3 as in :587-590)
+//   --benchmark, --accum-probe, --fp4-group-sweep: reported as not built
+//   success ends with "PASS"; a failure prints "error: <message>" on stderr
+//   and exits 1 (:83-88).
+//
+// Data follows the reference generators and seeds (main.swift:611-638,
+// 2785-2842): half x from the LCG with scale 1/8, packed FP4 weight bytes
+// from the LCG, E8M0 scales drawn from the pattern [124..130].  The format
+// rows quantize N(0, 0.02) weights as BASELINE configs[3] prescribes.
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "mxfp4hip.h"
+
+namespace {
+
+struct ProbeError {
+  std::string message;
+};
+
+[[noreturn]] void fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  throw ProbeError{buf};
+}
+
+std::vector<std::string> g_args;
+
+bool has_flag(const char* name) {
+  for (const std::string& a : g_args)
+    if (a == name) return true;
+  return false;
+}
+
+// intArgument (main.swift:2886-2892): "--name=value", default when absent or
+// not an integer.
+long int_argument(const char* name, long default_value) {
+  const std::string prefix = std::string(name) + "=";
+  for (const std::string& a : g_args) {
+    if (a.compare(0, prefix.size(), prefix) == 0) {
+      const char* s = a.c_str() + prefix.size();
+      char* end = nullptr;
+      const long v = std::strtol(s, &end, 10);
+      return (end && *end == '\0' && end != s) ? v : default_value;
+    }
+  }
+  return default_value;
+}
+
+void check(mx_ctx* ctx, int rc) {
+  if (rc != MX_OK) throw ProbeError{ctx ? mx_last_error(ctx) : mx_status_string(rc)};
+}
+
+// Value formatting of the KAT printout (format / formatHex, :302-316).
+std::string format_values(const std::vector<float>& v) {
+  std::string out;
+  char buf[64];
+  for (size_t i = 0; i < v.size(); i++) {
+    const float x = v[i];
+    if (std::isinf(x)) std::snprintf(buf, sizeof buf, "%s", x < 0 ? "-inf" : "inf");
+    else if (std::nearbyint(x) == x) std::snprintf(buf, sizeof buf, "%.0f", x);
+    else std::snprintf(buf, sizeof buf, "%.6g", x);
+    if (i) out += ", ";
+    out += buf;
+  }
+  return out;
+}
+
+std::string format_hex(const std::vector<uint8_t>& b) {
+  std::string out;
+  char buf[8];
+  for (size_t i = 0; i < b.size(); i++) {
+    std::snprintf(buf, sizeof buf, "%s%02X", i ? " " : "", b[i]);
+    out += buf;
+  }
+  return out;
+}
+
+struct KatCase {
+  const char* name;
+  int fmt;
+  std::vector<float> inputs, expected;
+  size_t packed_bytes;
+};
+
+// Packed numeric probe (runPackedNumericProbe, :91-162).  Returns true when
+// every roundtrip matches.
+bool run_kats(mx_ctx* ctx) {
+  const KatCase cases[] = {
+      {"FP4 E2M1", MX_FMT_FP4_E2M1,
+       {-8, -6, -4, -3, -2, -1.5f, -1, -0.5f, 0, 0.5f, 1, 1.5f, 2, 3, 4, 8},
+       {-6, -6, -4, -3, -2, -1.5f, -1, -0.5f, 0, 0.5f, 1, 1.5f, 2, 3, 4, 6}, 8},
+      {"FP8 E4M3", MX_FMT_FP8_E4M3,
+       {-512, -448, -16, -0.5f, 0, 0.125f, 16, 512},
+       {-448, -448, -16, -0.5f, 0, 0.125f, 16, 448}, 8},
+      {"FP8 E5M2", MX_FMT_FP8_E5M2,
+       {-57344, -1024, -2, -0.5f, 0, 0.25f, 1024, 57344},
+       {-57344, -1024, -2, -0.5f, 0, 0.25f, 1024, 57344}, 8},
+  };
+  bool all = true;
+  for (const KatCase& c : cases) {
+    std::vector<uint8_t> packed(c.packed_bytes);
+    std::vector<float> out(c.inputs.size());
+    check(ctx, mx_roundtrip(ctx, c.fmt, c.inputs.data(), c.inputs.size(), packed.data(), out.data()));
+    bool ok = true;
+    for (size_t i = 0; i < out.size(); i++) ok = ok && out[i] == c.expected[i];
+    all = all && ok;
+    std::printf("\n[%s] %s\n", ok ? "ok" : "FAIL", c.name);
+    std::printf("  input:    %s\n", format_values(c.inputs).c_str());
+    std::printf("  unpacked: %s\n", format_values(out).c_str());
+    std::printf("  expected: %s\n", format_values(c.expected).c_str());
+    std::printf("  bytes:    %s\n", format_hex(packed).c_str());
+  }
+  return all;
+}
+
+// ---- MLP benchmark --------------------------------------------------------
+
+struct Dev {  // device buffer owned by the driver
+  mx_ctx* ctx = nullptr;
+  void* p = nullptr;
+  Dev(mx_ctx* c, size_t bytes) : ctx(c) { check(ctx, mx_alloc(ctx, bytes, &p)); }
+  ~Dev() {
+    if (p) mx_free(ctx, p);
+  }
+  Dev(const Dev&) = delete;
+  Dev& operator=(const Dev&) = delete;
+};
+
+struct RowResult {
+  std::string name;
+  double seconds;
+  int iterations;
+  std::string checksum;
+};
+
+float half_to_float(uint16_t h) {
+  const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0) {
+    if (m == 0) bits = s;
+    else {  // subnormal
+      float f = std::ldexp((float)m, -24);
+      std::memcpy(&bits, &f, 4);
+      bits |= s;
+    }
+  } else if (e == 31) {
+    bits = s | 0x7f800000u | (m << 13);
+  } else {
+    bits = s | ((e + 112) << 23) | (m << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+// sampleFloatChecksum (:2844-2856) over an f32 or f16 output.
+std::string checksum(mx_ctx* ctx, const void* dev_out, size_t count, bool f16) {
+  std::vector<float> host(count);
+  if (f16) {
+    std::vector<uint16_t> h(count);
+    check(ctx, mx_download(ctx, h.data(), dev_out, count * 2));
+    for (size_t i = 0; i < count; i++) host[i] = half_to_float(h[i]);
+  } else {
+    check(ctx, mx_download(ctx, host.data(), dev_out, count * 4));
+  }
+  int samples = 0;
+  const double sum = mx_checksum_f32(host.data(), count, &samples);
+  char buf[96];
+  std::snprintf(buf, sizeof buf, "%.6g over %d samples", sum, samples);
+  return buf;
+}
+
+// printMLPBenchmarkResult (:2763-2770).
+void print_row(const RowResult& r, long tokens, long hidden, long inter) {
+  const double macs = 3.0 * tokens * hidden * inter * r.iterations;
+  const double tops = macs * 2.0 / r.seconds / 1e12;
+  std::printf("  %s:\n", r.name.c_str());
+  std::printf("    %.3f ms/MLP, %.3f effective TOPS\n", r.seconds * 1000.0 / r.iterations, tops);
+  std::printf("    checksum: %s\n", r.checksum.c_str());
+  std::fflush(stdout);
+}
+
+// printRelativeSlowdowns (:2772-2783).
+void print_slowdowns(const std::vector<RowResult>& rows) {
+  if (rows.empty()) return;
+  const RowResult* best = &rows[0];
+  for (const RowResult& r : rows)
+    if (r.seconds / r.iterations < best->seconds / best->iterations) best = &r;
+  const double b = best->seconds / best->iterations;
+  std::printf("  relative slowdown, best = %s:\n", best->name.c_str());
+  for (const RowResult& r : rows) std::printf("    %s: %.2fx\n", r.name.c_str(), (r.seconds / r.iterations) / b);
+}
+
+void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long iterations) {
+  std::printf("\nGated MLP benchmark:\n");
+  std::printf("  op: down(silu(gate(x)) * up(x))\n");
+  std::printf("  shape: tokens=%ld, hidden=%ld, intermediate=%ld\n", tokens, hidden, inter);
+  std::printf("  iterations: %ld\n", iterations);
+  const size_t T = tokens, H = hidden, I = inter;
+  const mx_mlp_config cfg{(uint32_t)T, (uint32_t)H, (uint32_t)I};
+  const int iters = (int)iterations;
+
+  // Reference inputs (main.swift:611-638).
+  std::vector<uint16_t> x_host(T * H);
+  mx_lcg_half(0x11112222u, x_host.size(), 0.125f, x_host.data());
+  Dev x(ctx, T * H * 2), out(ctx, T * H * 4);
+  check(ctx, mx_upload(ctx, x.p, x_host.data(), x_host.size() * 2));
+
+  std::vector<RowResult> rows;
+  auto record = [&](RowResult r) {
+    print_row(r, tokens, hidden, inter);
+    rows.push_back(std::move(r));
+  };
+
+  if (H % 64 == 0 && I % 64 == 0) {
+    const uint8_t pattern[] = {124, 125, 126, 127, 127, 128, 128, 129, 130};
+    const uint32_t data_seeds[3] = {0xabcd1357u, 0x2468bdf0u, 0x0badcafeu};
+    const uint32_t scale_seeds[3] = {0x7777ddddu, 0x8888eeeeu, 0x9999ffffu};
+    const size_t elems = I * H;
+    Dev q0(ctx, elems / 2), q1(ctx, elems / 2), q2(ctx, elems / 2);
+    Dev s0(ctx, elems / 32), s1(ctx, elems / 32), s2(ctx, elems / 32);
+    Dev* qs[3] = {&q0, &q1, &q2};
+    Dev* ss[3] = {&s0, &s1, &s2};
+    std::vector<uint8_t> host(elems / 2);
+    for (int m = 0; m < 3; m++) {
+      mx_lcg_bytes(data_seeds[m], elems / 2, host.data());
+      check(ctx, mx_upload(ctx, qs[m]->p, host.data(), elems / 2));
+      mx_lcg_pattern(scale_seeds[m], elems / 32, pattern, 9, host.data());
+      check(ctx, mx_upload(ctx, ss[m]->p, host.data(), elems / 32));
+    }
+    const mx_mlp_weights w{{q0.p, s0.p}, {q1.p, s1.p}, {q2.p, s2.p}};
+    struct Variant {
+      int id;
+      const char* name;
+      bool f16_out;
+    };
+    const Variant variants[] = {
+        {MX_MLP_REFROW,
+         "MXFP4 fused (FP4 + E8M0 decoded in registers, fp16 MFMA, reference epilogue): h_mxfp4_f", false},
+        {MX_MLP_FUSED, "MXFP4 fused (plain SwiGLU, fp16 out): h_mxfp4_h", true},
+        {MX_MLP_DEQUANT, "MXFP4 dequant (v_cvt_scalef32_pk_f16_fp4 -> half) + h_h_f", true},
+        {MX_MLP_W4A4, "MXFP4 W4A4 (x, mid -> MXFP4; FP4 x FP4 scaled MFMA): fp4_fp4_h", true},
+    };
+    for (const Variant& v : variants) {
+      if (v.id == MX_MLP_W4A4 && (H % 128 || I % 128)) {
+        std::printf("  W4A4 row: skipped; hidden and intermediate must be multiples of 128.\n");
+        continue;
+      }
+      double secs = 0.0;
+      // warm-up 1, then `iterations` back to back from one graph (the
+      // reference encodes them into one command buffer, :2062-2117)
+      check(ctx, mx_mlp_benchmark(ctx, v.id, &cfg, x.p, &w, 1, out.p, 1, iters, 1, &secs, nullptr, nullptr));
+      record({v.name, secs, iters, checksum(ctx, out.p, T * H, v.f16_out)});
+    }
+  } else {
+    std::printf("  MXFP4 rows: skipped; hidden and intermediate must be multiples of 64.\n");
+  }
+
+  if (H % 64 == 0 && I % 64 == 0) {
+    struct Fmt {
+      int id;
+      const char* name;
+    };
+    const Fmt fmts[] = {
+        {MX_WFMT_FP8_E4M3, "FP8 E4M3 weights (row scale): h_fp8_h"},
+        {MX_WFMT_FP8_E5M2, "FP8 E5M2 weights (row scale): h_fp8e5m2_h"},
+        {MX_WFMT_INT8, "INT8 weights (row scale): h_i8_h"},
+        {MX_WFMT_INT4, "INT4 weights (f16 scale per 32): h_i4_h"},
+        {MX_WFMT_W8A8, "W8A8 MLP: i8 x int8_t -> i32"},
+    };
+    Dev wf(ctx, I * H * 4);
+    for (const Fmt& f : fmts) {
+      if (f.id == MX_WFMT_W8A8 && (H % 128 || I % 128)) {
+        std::printf("  W8A8 row: skipped; hidden and intermediate must be multiples of 128.\n");
+        continue;
+      }
+      const bool i4 = f.id == MX_WFMT_INT4;
+      const size_t qb = i4 ? I * H / 2 : I * H;
+      Dev q0(ctx, qb), q1(ctx, qb), q2(ctx, qb);
+      const size_t sb_gu = i4 ? I * (H / 32) * 2 : I * 4, sb_dn = i4 ? H * (I / 32) * 2 : H * 4;
+      Dev s0(ctx, sb_gu), s1(ctx, sb_gu), s2(ctx, sb_dn);
+      Dev* qs[3] = {&q0, &q1, &q2};
+      Dev* ss[3] = {&s0, &s1, &s2};
+      for (int m = 0; m < 3; m++) {
+        const int rows_n = m < 2 ? (int)I : (int)H, k = m < 2 ? (int)H : (int)I;
+        check(ctx, mx_fill_normal(ctx, wf.p, MX_DTYPE_F32, (size_t)rows_n * k, 0x5eed0000ull + 16 * f.id + m, 0.0f,
+                                  0.02f));
+        check(ctx, mx_fmt_quantize(ctx, f.id, static_cast<const float*>(wf.p), rows_n, k, qs[m]->p, ss[m]->p));
+      }
+      const mx_mlp_weights w{{q0.p, s0.p}, {q1.p, s1.p}, {q2.p, s2.p}};
+      double secs = 0.0;
+      check(ctx, mx_fmt_mlp_benchmark(ctx, f.id, &cfg, x.p, &w, 1, out.p, 1, iters, 1, &secs));
+      record({f.name, secs, iters, checksum(ctx, out.p, T * H, true)});
+    }
+  }
+  print_slowdowns(rows);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  for (int i = 1; i < argc; i++) g_args.emplace_back(argv[i]);
+  mx_ctx* ctx = nullptr;
+  try {
+    // Argument checks of runMLPBenchmark (:592-597), done before the device
+    // is opened so that a bad command line fails the same way everywhere.
+    const bool mlp = has_flag("--mlp-benchmark");
+    const long tokens = int_argument("--mlp-tokens", 128);
+    const long hidden = int_argument("--mlp-hidden", 1024);
+    const long inter = int_argument("--mlp-intermediate", hidden * 4);
+    const long iterations = int_argument("--mlp-iterations", 3);
+    if (mlp) {
+      if (tokens <= 0 || hidden <= 0 || inter <= 0 || iterations <= 0)
+        fail("MLP sizes and iterations must be positive.");
+      if (hidden % 16 || inter % 16)
+        fail("MLP hidden and intermediate sizes must be multiples of 16 for packed FP4 weights.");
+    }
+
+    const int rc = mx_create(0, &ctx);
+    if (rc != MX_OK) fail("%s", mx_status_string(rc));
+    char name[256];
+    int cus = 0, mhz = 0;
+    check(ctx, mx_device_info(ctx, name, sizeof name, &cus, &mhz));
+    std::printf("Device: %s\n", name);
+    std::printf("Compute units: %d, max clock: %d MHz\n", cus, mhz);
+    std::fflush(stdout);
+
+    const bool kats_ok = run_kats(ctx);
+    if (has_flag("--skip-tensor")) std::printf("Tensor creation probe: skipped by --skip-tensor.\n");
+    else std::printf("Tensor creation probe: not applicable (no tensor objects on ROCm).\n");
+    if (has_flag("--benchmark") || has_flag("--fp4-group-sweep"))
+      std::printf("Scalar matmul benchmark: not part of this build.\n");
+    if (mlp) run_mlp_benchmark(ctx, tokens, hidden, inter, iterations);
+    if (has_flag("--accum-probe")) std::printf("Accumulator probe: not part of this build.\n");
+    if (!kats_ok) fail("One or more packed numeric checks failed.");
+    std::printf("PASS\n");
+  } catch (const ProbeError& e) {
+    std::fflush(stdout);
+    std::fprintf(stderr, "error: %s\n", e.message.c_str());
+    if (ctx) mx_destroy(ctx);
+    return 1;
+  }
+  mx_destroy(ctx);
+  return 0;
+}

@@ -1,0 +1,54 @@
+"""The command-line host driver (counterpart of the reference's MetalFP41Probe
+executable, Sources/MetalFP41Probe/main.swift): flag surface, error path
+(`error: <message>` on stderr, exit 1, main.swift:83-88) and, on the GPU, the
+full probe ending in PASS with the reference checksum 403573 on the fused
+MXFP4 row (README.md:292-294)."""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DRIVER = os.path.join(ROOT, "mpp-4.1-fp4-fp8-block_amd", "lib", "mxfp4_probe")
+
+needs_driver = pytest.mark.skipif(not os.path.exists(DRIVER), reason="driver not built (run build())")
+
+
+def run(*args, timeout=120):
+    return subprocess.run([DRIVER, *args], capture_output=True, text=True, timeout=timeout)
+
+
+@needs_driver
+@pytest.mark.parametrize("args,message", [
+    (["--mlp-benchmark", "--mlp-hidden=100"],
+     "MLP hidden and intermediate sizes must be multiples of 16 for packed FP4 weights."),
+    (["--mlp-benchmark", "--mlp-tokens=0"], "MLP sizes and iterations must be positive."),
+    (["--mlp-benchmark", "--mlp-iterations=-2"], "MLP sizes and iterations must be positive."),
+])
+def test_driver_rejects_bad_arguments(args, message):
+    # checked before the device is opened (main.swift:592-597), so this runs anywhere
+    r = run(*args)
+    assert r.returncode == 1
+    assert r.stderr.strip() == f"error: {message}"
+
+
+@needs_driver
+@pytest.mark.gpu
+def test_driver_mlp_benchmark_on_gpu():
+    r = run("--mlp-benchmark", "--mlp-iterations=2", "--skip-tensor", timeout=300)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    out = r.stdout
+    for name in ("FP4 E2M1", "FP8 E4M3", "FP8 E5M2"):
+        assert f"[ok] {name}" in out
+    assert "bytes:    FF DE BC 9A 10 32 54 76" in out          # E2M1 KAT bytes
+    assert "bytes:    FE FE D8 B0 00 20 58 7E" in out          # E4M3 KAT bytes
+    assert "shape: tokens=128, hidden=1024, intermediate=4096" in out
+    assert out.rstrip().endswith("PASS")
+    # reference fused-row checksum over the reference LCG data
+    m = re.search(r"reference epilogue\): h_mxfp4_f:\n.*\n\s+checksum: ([-0-9.e+]+) over 32 samples", out)
+    assert m, out
+    assert abs(float(m.group(1)) - 403573) / 403573 < 2e-5
+    for row in ("W4A4", "FP8 E5M2 weights", "INT4 weights", "W8A8 MLP", "relative slowdown"):
+        assert row in out
