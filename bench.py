@@ -127,6 +127,36 @@ def cpu_baseline(T, H, I, budget_s=12.0):
                       f"float64 accumulation, {threads} threads), ~{el:.0f} s"}
 
 
+def copy_probe(nbytes=256 << 20, reps=3):
+    """A plain copy kernel of known size, for calibrating the HBM traffic
+    counters: every dispatch reads and writes exactly `nbytes`."""
+    import torch
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": nbytes, "dispatches": reps}), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_mxfp4_gate_up_swiglu_c1_t1_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel, as recorded from two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) scaled by the copy
+    kernel; None when no such record exists."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,7 +164,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="",
+                    help="comma-separated secondary configs to run (c1_t8,c4,c0,c2,c3); default all")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run only a 256 MiB device-to-device copy x3 (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the MXFP4 MLP hot path is a single-GPU kernel; see DESIGN.md for how it shards).",
@@ -157,7 +195,7 @@ def main():
     mlp_bytes = 3 * mxfp4_bytes(I, H) + 2 * T * H * 2 + 2 * T * I * 2
     achieved = gu_bytes / (gu_us * 1e-6)
     roofline = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": measured_traffic(),
                 "kernel": gu_name, "algorithmic_bytes": gu_bytes,
                 "kernel_us": round(gu_us, 3)}
     result = {
@@ -177,22 +215,32 @@ def main():
 
     if not args.no_secondary:
         sec = {}
-        r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2)
-        b = 3 * mxfp4_bytes(2048, 7168) + 2 * 8 * 7168 * 2 + 2 * 8 * 2048 * 2
-        r["hbm_frac"] = round(b / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
-        sec["c1_t8_fused"] = r
-        r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, 1, 10, 2, seed=4)
-        r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
-        sec["c4_w4a4"] = r
+        only = set(t for t in args.only.split(",") if t)
+        want = lambda tag: not only or tag in only
+        if want("c1_t8"):
+            r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2)
+            b = 3 * mxfp4_bytes(2048, 7168) + 2 * 8 * 7168 * 2 + 2 * 8 * 2048 * 2
+            r["hbm_frac"] = round(b / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
+            sec["c1_t8_fused"] = r
+        if want("c4"):
+            r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, 1, 10, 2, seed=4)
+            r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
+            sec["c4_w4a4"] = r
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_W4A4, "w4a4")):
+            if not want("c0"):
+                break
             r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, 24, 100, 10, seed=5)
             sec[f"c0_{tag}"] = r
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant")):
+            if not want("c2"):
+                break
             r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, 24, 100, 10, seed=6)
             r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
             sec[f"c2_{tag}"] = r
         for wfmt, tag in ((M.WFMT_FP8_E4M3, "fp8_e4m3"), (M.WFMT_FP8_E5M2, "fp8_e5m2"),
                           (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32"), (M.WFMT_W8A8, "w8a8")):
+            if not want("c3"):
+                break
             r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, 2, 40, 4, seed=7,
                               wfmt=wfmt)
             wb = 3 * 4096 * 14336 * (0.5 if wfmt == M.WFMT_INT4 else 1)
