@@ -17,11 +17,12 @@
 //               feeds v_mfma_f32_16x16x32_f16 (tokens padded to 16 rows; the
 //               MFMA is never the bottleneck).  The activations follow the
 //               same K permutation.
-//   order     = every weight load of the wave is issued first (scheduling
-//               barriers keep the order, so the compiler's waits release the
-//               steps one by one); while they are in flight the workgroup
-//               stages the activations and its rows' E8M0 scales in LDS with
-//               coalesced loads, so the per-step operand reads are ds_reads.
+//   order     = the activations (LDS DMA) and the rows' E8M0 scales are
+//               requested first, then every weight load of the wave
+//               (scheduling barriers keep the order).  vmcnt retires in
+//               order, so the staging can be waited for and written to LDS
+//               while the weights are still in flight; the compiler's
+//               per-step waits then release the MFMA steps one by one.
 //   reduction = the W partial 16x16 tiles are added in LDS in wave order
 //               (deterministic), then the epilogue writes f16:
 //                 single: out[t][n] = sum
@@ -39,6 +40,15 @@ namespace mx {
 constexpr int kStepK = 128;   // K per lane step: 4 lane groups x 32-element blocks
 // NSTEP: steps per wave whose weight loads are issued together (2, 4 or 8).
 constexpr int kW = 8;         // waves per workgroup
+constexpr int kMaxScaleRegs = 4;  // scale dwords staged per thread: K <= 16384
+
+// 16-byte global -> LDS DMA of one lane (LDS base wave-uniform).
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt(n), expcnt and lgkmcnt untouched.
+constexpr int gemv_wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // Dynamic LDS layout: [scales 16 rows x K/32 bytes][x T rows x (K+8) halves]
 // [reduction W x 16 x 17 floats].
@@ -78,7 +88,33 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
   row_ptrs(r, wrow, srow);
   wrow += lg * 16;
 
-  // 1) Issue this wave's first batch of weight loads.
+  // 1) Staging first: x rows go global -> LDS by DMA (no registers), the 16
+  //    rows' scales into a few registers.  Issued before the weight loads,
+  //    they complete first (vmcnt retires in order), so waiting for them
+  //    does not wait for the weights.
+  {
+    const int xrow_b = K * 2, xchunks = (xrow_b + 1023) / 1024;
+    for (int i = wave; i < T * xchunks; i += kW) {  // wave-uniform
+      const int t = i / xchunks, c = i % xchunks;
+      if (c * 1024 + lane * 16 < xrow_b)
+        dma16(reinterpret_cast<const uint8_t*>(g.x) + (size_t)t * xrow_b + c * 1024 + lane * 16,
+              reinterpret_cast<uint8_t*>(x_lds) + (size_t)t * (K + 8) * 2 + c * 1024);
+    }
+  }
+  const int n_sdw = 16 * (KB / 4);  // scale dwords of the 16 rows
+  uint32_t sreg[kMaxScaleRegs];
+#pragma unroll
+  for (int q = 0; q < kMaxScaleRegs; q++) {
+    const int i = min(tid + q * 64 * kW, n_sdw - 1);  // clamped: no predicated loads
+    const int rr = i / (KB / 4), c = i % (KB / 4);
+    const uint8_t* w;
+    const uint8_t* s;
+    row_ptrs(rr, w, s);
+    sreg[q] = *reinterpret_cast<const uint32_t*>(s + c * 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2) This wave's first batch of weight loads.
   uint4 wv[NSTEP];
 #pragma unroll
   for (int b = 0; b < NSTEP; b++) {
@@ -87,21 +123,22 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
     wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // 2) While they are in flight, stage x [T][K] and the 16 rows' scales.
-  for (int i = tid; i < T * (K / 8); i += 64 * kW) {
-    const int t = i / (K / 8), c = i % (K / 8);
-    *reinterpret_cast<uint4*>(x_lds + (size_t)t * (K + 8) + c * 8) =
-        *reinterpret_cast<const uint4*>(g.x + (size_t)t * K + c * 8);
+
+  // 3) Staging landed (only the NSTEP weight loads may still be in flight):
+  //    scales to LDS, then a bare barrier (__syncthreads would also wait for
+  //    the weights).
+  __builtin_amdgcn_s_waitcnt(gemv_wait_vm(NSTEP));
+#pragma unroll
+  for (int q = 0; q < kMaxScaleRegs; q++) {
+    const int i = tid + q * 64 * kW;
+    if (i < n_sdw) {
+      const int rr = i / (KB / 4), c = i % (KB / 4);
+      *reinterpret_cast<uint32_t*>(s_lds + (size_t)rr * KB + c * 4) = sreg[q];
+    }
   }
-  for (int i = tid; i < 16 * (KB / 4); i += 64 * kW) {
-    const int rr = i / (KB / 4), c = i % (KB / 4);
-    const uint8_t* w;
-    const uint8_t* s;
-    row_ptrs(rr, w, s);
-    *reinterpret_cast<uint32_t*>(s_lds + (size_t)rr * KB + c * 4) =
-        *reinterpret_cast<const uint32_t*>(s + c * 4);
-  }
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(gemv_wait_vm(NSTEP) & ~(15 << 8));  // + lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 
   // Lane r feeds activation row r; rows >= T re-read row T-1 (their MFMA rows
   // are never stored), so no load or read is predicated.
@@ -198,7 +235,7 @@ static hipError_t launch_ns(const GemvArgs& g, size_t lds, hipStream_t st) {
 // redundant loads when K is short.
 hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
   const size_t lds = gemv_lds_bytes(g.t, g.k);
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (lds > 160 * 1024 || g.k > 16384 || g.k % kStepK) return hipErrorInvalidValue;
   const int per_wave = (g.k / kStepK + kW - 1) / kW;
   if (per_wave <= 2) return dual ? launch_ns<true, 2>(g, lds, st) : launch_ns<false, 2>(g, lds, st);
   if (per_wave <= 4) return dual ? launch_ns<true, 4>(g, lds, st) : launch_ns<false, 4>(g, lds, st);
