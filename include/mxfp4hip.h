@@ -182,8 +182,9 @@ int mx_mlp_benchmark(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const v
                      const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
                      int iterations, int use_graph, double* seconds_out, double* kernel_us_out,
                      int* n_kernels_out);
-/* Name of kernel `index` of a variant's forward (for the per-kernel times). */
-const char* mx_mlp_kernel_name(int variant, int tokens, int index);
+/* Name of kernel `index` of the forward that `variant` runs at shape `cfg`
+ * (for the per-kernel times); NULL past the last kernel. */
+const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index);
 
 /* ---- weight-format rows (config 3) ------------------------------------------ */
 /* Quantize f32 weights [rows][k] into format `wfmt` (scales per the enum). */

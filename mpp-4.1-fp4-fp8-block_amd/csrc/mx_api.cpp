@@ -96,11 +96,24 @@ int check_mlp_cfg(mx_ctx* c, int variant, const mx_mlp_config* cfg) {
 }
 
 bool gemv_ok(const mx_mlp_config* cfg) {
-  // decode GEMV: <= 16 tokens, K multiples of 128, and the activations plus
-  // one row group's scales fit the workgroup's LDS
+  // decode GEMV: <= 16 tokens, K multiples of 128 up to 16384, and the
+  // activations plus one row group's scales fit the workgroup's LDS
   return cfg->tokens <= 16 && cfg->hidden % 128 == 0 && cfg->intermediate % 128 == 0 &&
+         cfg->hidden <= 16384 && cfg->intermediate <= 16384 &&
          mx::gemv_lds_need((int)cfg->tokens, (int)cfg->hidden) <= 160 * 1024 &&
          mx::gemv_lds_need((int)cfg->tokens, (int)cfg->intermediate) <= 160 * 1024;
+}
+
+// Which kernels a forward runs (shared by the launcher and the name query).
+enum MlpPath { PATH_GEMV, PATH_GEMM_Q, PATH_REFROW, PATH_DEQUANT, PATH_W4A4 };
+
+MlpPath mlp_path(int variant, const mx_mlp_config* cfg) {
+  switch (variant) {
+    case MX_MLP_FUSED: return gemv_ok(cfg) ? PATH_GEMV : PATH_GEMM_Q;
+    case MX_MLP_REFROW: return PATH_REFROW;
+    case MX_MLP_DEQUANT: return PATH_DEQUANT;
+    default: return PATH_W4A4;
+  }
 }
 
 // Scratch layout for one variant; returns bytes needed.
@@ -176,15 +189,16 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
   const uint8_t* wd = static_cast<const uint8_t*>(w->down.data);
   const uint8_t* sd = static_cast<const uint8_t*>(w->down.scales);
 
-  if (variant == MX_MLP_FUSED && gemv_ok(cfg)) {
+  const MlpPath path = mlp_path(variant, cfg);
+  if (path == PATH_GEMV) {
     uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
     mx::GemvArgs gu{static_cast<const uint16_t*>(x), wg, sg, wu, su, mid, T, I, H};
     mx::GemvArgs dn{mid, wd, sd, nullptr, nullptr, static_cast<uint16_t*>(out), T, H, I};
     steps.push_back({"gemv_mxfp4_gate_up_swiglu", [=] { return mx::launch_gemv_mxfp4(1, gu, st); }});
     steps.push_back({"gemv_mxfp4_down", [=] { return mx::launch_gemv_mxfp4(0, dn, st); }});
-  } else if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
+  } else if (path == PATH_GEMM_Q || path == PATH_REFROW) {
     uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
-    const bool ref = variant == MX_MLP_REFROW;
+    const bool ref = path == PATH_REFROW;
     const int e_gu = ref ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16;
     const int e_dn = ref ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
     void* qws = ws + s.qws;
@@ -194,7 +208,7 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
                      [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_MXFP4, e_gu, gu, st); }});
     steps.push_back({ref ? "gemm_q_mxfp4_down_f32" : "gemm_q_mxfp4_down",
                      [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_MXFP4, e_dn, dn, st); }});
-  } else if (variant == MX_MLP_DEQUANT) {
+  } else if (path == PATH_DEQUANT) {
     uint16_t* wg16 = reinterpret_cast<uint16_t*>(ws + s.wg);
     uint16_t* wu16 = reinterpret_cast<uint16_t*>(ws + s.wu);
     uint16_t* wd16 = reinterpret_cast<uint16_t*>(ws + s.wd);
@@ -517,19 +531,20 @@ int mx_mlp_forward(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void*
   return run_steps(c, steps);
 }
 
-const char* mx_mlp_kernel_name(int variant, int tokens, int index) {
-  static const char* fused_gemv[] = {"gemv_mxfp4_gate_up_swiglu", "gemv_mxfp4_down"};
+const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index) {
+  static const char* gemv[] = {"gemv_mxfp4_gate_up_swiglu", "gemv_mxfp4_down"};
   static const char* fused[] = {"gemm_q_mxfp4_gate_up_swiglu", "gemm_q_mxfp4_down"};
   static const char* ref[] = {"gemm_q_mxfp4_gate_up_swiglu_half", "gemm_q_mxfp4_down_f32"};
   static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
                               "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
   static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down"};
-  if (index < 0) return nullptr;
-  switch (variant) {
-    case MX_MLP_FUSED: return index < 2 ? (tokens <= 16 ? fused_gemv[index] : fused[index]) : nullptr;
-    case MX_MLP_REFROW: return index < 2 ? ref[index] : nullptr;
-    case MX_MLP_DEQUANT: return index < 7 ? deq[index] : nullptr;
-    case MX_MLP_W4A4: return index < 3 ? w4[index] : nullptr;
+  if (index < 0 || !cfg || variant < MX_MLP_FUSED || variant > MX_MLP_REFROW) return nullptr;
+  switch (mlp_path(variant, cfg)) {
+    case PATH_GEMV: return index < 2 ? gemv[index] : nullptr;
+    case PATH_GEMM_Q: return index < 2 ? fused[index] : nullptr;
+    case PATH_REFROW: return index < 2 ? ref[index] : nullptr;
+    case PATH_DEQUANT: return index < 7 ? deq[index] : nullptr;
+    case PATH_W4A4: return index < 3 ? w4[index] : nullptr;
   }
   return nullptr;
 }

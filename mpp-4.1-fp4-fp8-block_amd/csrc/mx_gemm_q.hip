@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemmArgs g) {
         for (int v = 0; v < 16; v++) {
           // copy the vector element to a scalar first: __builtin_bit_cast of
           // a vector-element subscript yields element 0 for every v
-          const auto ge = acc[i][jj][v], ue = acc[i][1][v];
+          const auto ge = acc[i][jj][v], ue = acc[i][NWB - 1][v];
           gv[v] = __builtin_bit_cast(uint32_t, ge);
           uv[v] = DUAL ? __builtin_bit_cast(uint32_t, ue) : 0u;
         }
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(QGemmArgs g) {
         const float x0 = scaled<AK, BK>(g0, g, reinterpret_cast<const float*>(g.s0), row, col);
         float u = 0.0f;
         if (DUAL) {
-          const float u0 = AK == AK_I8 ? (float)(int)acc[i][1][v] : (float)acc[i][1][v];
+          const float u0 = AK == AK_I8 ? (float)(int)acc[i][NWB - 1][v] : (float)acc[i][NWB - 1][v];
           u = scaled<AK, BK>(u0, g, reinterpret_cast<const float*>(g.s1), row, col);
         }
         epi_store<EPI>(g.c, o, x0, u);

@@ -24,7 +24,7 @@
 //               while the weights are still in flight; the compiler's
 //               per-step waits then release the MFMA steps one by one.
 //   reduction = the W partial 16x16 tiles are added in LDS in wave order
-//               (deterministic), then the epilogue writes f16:
+//               (deterministic, one barrier), then the epilogue writes f16:
 //                 single: out[t][n] = sum
 //                 dual:   mid[t][c] = silu(sum_gate) * sum_up  (swiglu_float)
 //
@@ -193,25 +193,17 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
 #pragma unroll
   for (int v = 0; v < 4; v++) red[(wave * 16 + lg * 4 + v) * 17 + r] = acc0[v] + acc1[v];
   __syncthreads();
-  const int tt = tid >> 4, cc = tid & 15;
-  float tot = 0.0f;
-  if (tid < 256) {
+  if (tid < 256) {  // whole waves: thread (token tt, column cc)
+    const int tt = tid >> 4, cc = tid & 15;
+    float tot = 0.0f;
 #pragma unroll
     for (int w = 0; w < kW; w++) tot += red[(w * 16 + tt) * 17 + cc];
-  }
-  __syncthreads();
-  if (tid < 256) red[tt * 17 + cc] = tot;
-  __syncthreads();
-  if (DUAL) {
-    if (tid < 128) {
-      const int t = tid >> 3, j = tid & 7;
-      if (t < T) {
-        const float gv = red[t * 17 + j], uv = red[t * 17 + 8 + j];
-        g.out[(size_t)t * g.n + blockIdx.x * 8 + j] = f32_to_f16_bits(silu(gv) * uv);
-      }
+    if (DUAL) {
+      const float uv = __shfl_xor(tot, 8);  // column cc + 8 is the same channel's up sum
+      if (cc < 8 && tt < T) g.out[(size_t)tt * g.n + blockIdx.x * 8 + cc] = f32_to_f16_bits(silu(tot) * uv);
+    } else if (tt < T) {
+      g.out[(size_t)tt * g.n + blockIdx.x * 16 + cc] = f32_to_f16_bits(tot);
     }
-  } else {
-    if (tid < 256 && tt < T) g.out[(size_t)tt * g.n + blockIdx.x * 16 + cc] = f32_to_f16_bits(red[tt * 17 + cc]);
   }
 }
 

@@ -93,7 +93,7 @@ def load() -> ctypes.CDLL:
         "mx_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp, _int,
                                     _int, _int, P(ctypes.c_double), P(ctypes.c_double), P(_int)]),
-        "mx_mlp_kernel_name": (ctypes.c_char_p, [_int, _int, _int]),
+        "mx_mlp_kernel_name": (ctypes.c_char_p, [_int, ctypes.c_void_p, _int]),
         "mx_fmt_quantize": (_int, [_vp, _int, _vp, _int, _int, _vp, _vp]),
         "mx_fmt_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_fmt_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp,
@@ -266,7 +266,7 @@ class Device:
             self.ctx, variant, ctypes.byref(cfg), x.p, arr, len(sets), out.p, warmup, iterations,
             1 if graph else 0, ctypes.byref(secs), kus if per_kernel else None,
             ctypes.byref(nk) if per_kernel else None))
-        names = [load().mx_mlp_kernel_name(variant, tokens, i).decode() for i in range(nk.value)]
+        names = [load().mx_mlp_kernel_name(variant, ctypes.byref(cfg), i).decode() for i in range(nk.value)]
         return secs.value, dict(zip(names, list(kus)[:nk.value]))
 
     def fmt_quantize(self, wfmt, w: DevBuf, rows, k, q: DevBuf, scales: DevBuf):

@@ -199,5 +199,42 @@ def test_benchmark_entry_point(dev):
     out = dev.alloc(8 * 1024 * 2)
     secs, kern = dev.mlp_benchmark(M.MLP_FUSED, 8, 1024, 2048, d.x, [d.weights] * 2, out,
                                    warmup=1, iterations=5)
-    assert secs > 0 and len(kern) == 2 and all(v > 0 for v in kern.values()), kern
+    # 8 tokens: the decode GEMVs
+    assert secs > 0 and list(kern) == ["gemv_mxfp4_gate_up_swiglu", "gemv_mxfp4_down"], kern
+    assert all(v > 0 for v in kern.values()), kern
+    secs, kern = dev.mlp_benchmark(M.MLP_FUSED, 8, 1024, 2048, d.x, [d.weights] * 2, out,
+                                   warmup=1, iterations=5, graph=False)
+    assert secs > 0
+    dev.sync()
+    out.free()
     d.free()
+
+
+# ---- decode GEMV path (tokens <= 16) -----------------------------------------
+# Shapes: fewest workgroups (H = I = 128, down waves with no K step), several
+# load batches per wave (K = 8192 and 16384), the largest token count.
+@pytest.mark.parametrize("T,H,I", [(3, 128, 128), (4, 256, 8192), (1, 16384, 128), (16, 1024, 512)])
+def test_decode_gemv_shapes(dev, T, H, I):
+    d = MlpData(dev, T, H, I, seed=T + H // 128)
+    check(run_mlp(dev, d, M.MLP_FUSED), oracle_mlp(d, M.MLP_FUSED), what=f"decode T={T} H={H} I={I}")
+    d.free()
+
+
+def test_decode_back_to_back_distinct_inputs(dev):
+    """Consecutive forwards with different inputs share the context's mid
+    buffer; enqueued back to back, each must produce its own result."""
+    T, H, I = 2, 1024, 2048
+    a, b = MlpData(dev, T, H, I, seed=41), MlpData(dev, T, H, I, seed=43)
+    refs = [run_mlp(dev, a, M.MLP_FUSED), run_mlp(dev, b, M.MLP_FUSED)]
+    assert not np.array_equal(refs[0], refs[1])
+    outs = [dev.alloc(T * H * 2) for _ in range(24)]
+    for n, o in enumerate(outs):  # no host sync in between
+        d = (a, b)[n % 2]
+        dev.mlp_forward(M.MLP_FUSED, T, H, I, d.x, d.weights, o)
+    dev.sync()
+    for n, o in enumerate(outs):
+        got = dev.download(o, np.float16, (T, H))
+        assert np.array_equal(got.view(np.uint16), refs[n % 2].view(np.uint16)), n
+        o.free()
+    a.free()
+    b.free()
