@@ -152,6 +152,17 @@ int mx_gemm_f16(mx_ctx* ctx, const void* a, int a_dtype, const void* b, float* c
  * mpp_mlp_i8_i8_i32_n128 (MPPMLPKernels.metal:61-70), the W8A8 core.
  * n % 64 == 0, k % 128 == 0. */
 int mx_gemm_i8(mx_ctx* ctx, const int8_t* a, const int8_t* b, int32_t* c, int m, int n, int k);
+/* Accumulator-probe GEMM: the accum_{h_h,h_fp4,fp4_fp4,fp8_fp8}_{h,f}
+ * family (AccumProbeKernels.metal:41-127; ABI a, b, c, m, n, k).
+ * C[m][n] = sum_k A[m][k] * B[n][k], A [m][k] and B [n][k] K-contiguous in
+ * format a_fmt / b_fmt (MX_PROBE_*; FP4 is E2M1 two per byte, low nibble =
+ * even k; FP4 and FP8 carry no scales); f32 accumulation; C f32 or f16
+ * (c_dtype; f16 is one RNE rounding of the f32 sum, >= 65520 -> inf).
+ * Pairs: (F16, F16), (F16, FP4), (FP4, FP4), (FP8, FP8).  Any k >= 1 (even
+ * with FP4); n % 64 == 0; FP4 / FP8 A also needs m % 32 == 0. */
+enum { MX_PROBE_F16 = 0, MX_PROBE_FP4 = 1, MX_PROBE_FP8 = 2 };
+int mx_accum_gemm(mx_ctx* ctx, int a_fmt, const void* a, int b_fmt, const void* b, void* c,
+                  int c_dtype, int m, int n, int k);
 /* SwiGLU: variant 0 mpp_mlp_swiglu_float, 1 mpp_mlp_swiglu_half,
  * 2 mpp_mlp_swiglu_half_from_half, 3 mpp_mlp_swiglu_i8
  * (MPPMLPKernels.metal:186-257; ABI gate, up, mid, config). */

@@ -464,13 +464,16 @@ static int check_gemm(mx_ctx* c, int m, int n, int k, const void* a, const void*
 
 // One GEMM through the small-M family when the shape fits it (k % 64),
 // else through the K-step-32 kernel.
+// ws_off: bytes of the workspace the caller already uses (kept in front of
+// the split-K partials).
 static int run_gemm(mx_ctx* c, const void* a, int a_dtype, int bk, const void* b, const void* scales,
-                    void* out, int epi, int m, int n, int k) {
+                    void* out, int epi, int m, int n, int k, size_t ws_off = 0) {
   const int ak = a_dtype == MX_DTYPE_F32 ? mx::AK_F32 : mx::AK_F16;
   if (mx::gemm_q_ok(ak, bk, epi, m, n, k)) {
     const size_t wsb = mx::gemm_q_ws_bytes(ak, epi, m, n, k);
-    if (int rc = ensure_ws(c, wsb)) return rc;
-    mx::QGemmArgs g{a, nullptr, b, scales, nullptr, nullptr, out, wsb ? c->ws : nullptr, m, n, k, 0};
+    if (int rc = ensure_ws(c, ws_off + wsb)) return rc;
+    void* part = wsb ? static_cast<uint8_t*>(c->ws) + ws_off : nullptr;
+    mx::QGemmArgs g{a, nullptr, b, scales, nullptr, nullptr, out, part, m, n, k, 0};
     MX_HIP(c, mx::launch_gemm_q(ak, bk, epi, g, c->stream));
     return MX_OK;
   }
@@ -510,6 +513,61 @@ int mx_gemm_i8(mx_ctx* c, const int8_t* a, const int8_t* b, int32_t* out, int m,
   mx::QGemmArgs g{a, nullptr, b, nullptr, nullptr, nullptr, out, wsb ? c->ws : nullptr, m, n, k, 0};
   MX_HIP(c, mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_I32, g, c->stream));
   return MX_OK;
+}
+
+int mx_accum_gemm(mx_ctx* c, int a_fmt, const void* a, int b_fmt, const void* b, void* out, int c_dtype,
+                  int m, int n, int k) {
+  if (!c) return MX_EINVAL;
+  const bool hh = a_fmt == MX_PROBE_F16 && b_fmt == MX_PROBE_F16;
+  const bool hq = a_fmt == MX_PROBE_F16 && b_fmt == MX_PROBE_FP4;
+  const bool qq = (a_fmt == MX_PROBE_FP4 && b_fmt == MX_PROBE_FP4) || (a_fmt == MX_PROBE_FP8 && b_fmt == MX_PROBE_FP8);
+  if (!hh && !hq && !qq) return set_err(c, MX_EINVAL, "Unsupported probe operand pair (%d, %d).", a_fmt, b_fmt);
+  if (m <= 0 || n <= 0 || k <= 0) return set_err(c, MX_EINVAL, "matmul sizes must be positive.");
+  if (n % 64) return set_err(c, MX_EINVAL, "matmul n must be a multiple of 64.");
+  if (qq && m % 32) return set_err(c, MX_EINVAL, "FP4 / FP8 probe matmul needs m %% 32 == 0.");
+  if ((a_fmt == MX_PROBE_FP4 || b_fmt == MX_PROBE_FP4) && k % 2)
+    return set_err(c, MX_EINVAL, "packed FP4 rows need an even k.");
+  if (!a || !b || !out || !aligned16(a) || !aligned16(b) || !aligned16(out))
+    return set_err(c, MX_EINVAL, "matmul buffers must be non-null and 16-byte aligned.");
+  if (c_dtype != MX_DTYPE_F32 && c_dtype != MX_DTYPE_F16)
+    return set_err(c, MX_EINVAL, "probe C must be f32 or f16.");
+  const int epi = c_dtype == MX_DTYPE_F32 ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
+  // Workspace: [A padded][B padded][unit scale plane][split-K partials].  K
+  // is padded with zero codes to a multiple of 64 (the reference takes any
+  // dot length, e.g. 1022 or 1818), sized once so nothing moves in between.
+  auto row_bytes = [](int fmt, size_t kk) { return fmt == MX_PROBE_F16 ? kk * 2 : fmt == MX_PROBE_FP8 ? kk : kk / 2; };
+  const size_t kp = align_up((size_t)k, 64);
+  const bool pad = kp != (size_t)k;
+  const size_t a_sz = pad ? align_up((size_t)m * row_bytes(a_fmt, kp), 256) : 0;
+  const size_t b_sz = pad ? align_up((size_t)n * row_bytes(b_fmt, kp), 256) : 0;
+  const size_t plane = hq ? align_up((size_t)n * (kp / 32), 256) : 0;
+  const int bk = hq ? mx::BK_MXFP4 : mx::BK_F16;
+  const size_t part = (hh || hq) && mx::gemm_q_ok(mx::AK_F16, bk, epi, m, n, (int)kp)
+                          ? mx::gemm_q_ws_bytes(mx::AK_F16, epi, m, n, (int)kp) : 0;
+  if (int rc = ensure_ws(c, a_sz + b_sz + plane + part)) return rc;
+  uint8_t* ws = static_cast<uint8_t*>(c->ws);
+  const void* pa = a;
+  const void* pb = b;
+  if (pad) {
+    MX_HIP(c, mx::launch_pad_rows(static_cast<const uint8_t*>(a), m, row_bytes(a_fmt, k), ws,
+                                  row_bytes(a_fmt, kp), c->stream));
+    MX_HIP(c, mx::launch_pad_rows(static_cast<const uint8_t*>(b), n, row_bytes(b_fmt, k), ws + a_sz,
+                                  row_bytes(b_fmt, kp), c->stream));
+    pa = ws;
+    pb = ws + a_sz;
+  }
+  if (qq) {
+    MX_HIP(c, mx::launch_gemm_f8f6f4_unit(a_fmt == MX_PROBE_FP4, c_dtype == MX_DTYPE_F32,
+                                          static_cast<const uint8_t*>(pa), static_cast<const uint8_t*>(pb), out, m,
+                                          n, (int)kp, c->stream));
+    return MX_OK;
+  }
+  uint8_t* sc = nullptr;
+  if (hq) {  // unscaled FP4 = MXFP4 with every E8M0 byte 127 (1.0)
+    sc = ws + a_sz + b_sz;
+    MX_HIP(c, mx::launch_fill_u8(sc, (size_t)n * (kp / 32), 127, c->stream));
+  }
+  return run_gemm(c, pa, MX_DTYPE_F16, bk, pb, sc, out, epi, m, n, (int)kp, a_sz + b_sz + plane);
 }
 
 int mx_swiglu(mx_ctx* c, int variant, const void* gate, const void* up, void* mid, int tokens,

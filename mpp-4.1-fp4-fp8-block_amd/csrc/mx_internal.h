@@ -94,6 +94,16 @@ struct GemvArgs {
   int t, n, k;
 };
 hipError_t launch_gemv_mxfp4(int dual_swiglu, const GemvArgs& g, hipStream_t st);
+
+// Unscaled FP4 x FP4 / FP8 E4M3 x FP8 E4M3 GEMM for the accumulator probe
+// (mx_accum.hip): C f32 or f16 [m][n] = A [m][k] . B [n][k]^T.
+bool gemm_f8f6f4_unit_ok(int m, int n, int k);
+// Rows of rb bytes -> rows of rbp >= rb bytes, zero-filled (mx_accum.hip).
+hipError_t launch_pad_rows(const uint8_t* src, size_t rows, size_t rb, uint8_t* dst, size_t rbp, hipStream_t st);
+// dst[0, n) = value by a kernel (dst 4-byte aligned).
+hipError_t launch_fill_u8(uint8_t* dst, size_t n, uint8_t value, hipStream_t st);
+hipError_t launch_gemm_f8f6f4_unit(int fp4, int out_f32, const uint8_t* a, const uint8_t* b, void* c, int m,
+                                   int n, int k, hipStream_t st);
 size_t gemv_lds_need(int t, int k);  // dynamic LDS of one workgroup (<= 160 KB to run)
 
 // W4A4 FP4 x FP4 scaled-MFMA GEMM (mx_gemm_fp4.hip).

@@ -10,7 +10,9 @@
 //   --mlp-benchmark       gated MLP benchmark rows (runMLPBenchmark, :586-1521)
 //     --mlp-tokens=T --mlp-hidden=H --mlp-intermediate=I --mlp-iterations=N
 //     (defaults 128, 1024, 4*H, 3 as in :587-590)
-//   --benchmark, --accum-probe, --fp4-group-sweep: reported as not built
+//   --accum-probe         accumulator precision / overflow probe
+//                         (runAccumulatorProbe, :1523-1713)
+//   --benchmark, --fp4-group-sweep: reported as not built
 //   success ends with "PASS"; a failure prints "error: <message>" on stderr
 //   and exits 1 (:83-88).
 //
@@ -24,6 +26,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -317,6 +320,103 @@ void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long i
   print_slowdowns(rows);
 }
 
+// ---- accumulator precision / overflow probe -------------------------------
+// runAccumulatorProbe (main.swift:1523-1713): constant-fill 64 x 128 GEMMs of
+// dot length K with a half and a float destination, for half x half,
+// half x FP4, FP4 x FP4 and FP8 E4M3 x FP8 E4M3 (mx_accum_gemm).  Every C
+// element has the same exact value, so C[0] against K * product isolates the
+// accumulator and destination rounding.
+
+std::string format_value(double v) {  // formatValue (:1647-1658)
+  char buf[64];
+  if (std::isinf(v)) return v < 0 ? "-inf" : "inf";
+  if (std::isnan(v)) return "nan";
+  if (v == std::nearbyint(v) && std::fabs(v) < 1e15) std::snprintf(buf, sizeof buf, "%.0f", v);
+  else std::snprintf(buf, sizeof buf, "%.6g", v);
+  return buf;
+}
+
+void run_accum_probe(mx_ctx* ctx) {
+  const int m = 64, n = 128, max_k = 131072;
+  auto half_fill = [&](size_t count, uint16_t bits) {
+    std::vector<uint16_t> h(count, bits);
+    auto d = std::make_unique<Dev>(ctx, count * 2);
+    check(ctx, mx_upload(ctx, d->p, h.data(), count * 2));
+    return d;
+  };
+  auto byte_fill = [&](size_t count, int value) {
+    auto d = std::make_unique<Dev>(ctx, count);
+    check(ctx, mx_memset(ctx, d->p, value, count));
+    return d;
+  };
+  // 0x3c00 = half 1.0, 0x4800 = half 8.0; bytes 0x22 = two FP4 1.0,
+  // 0x77 = two FP4 6.0, 0x38 = E4M3 1.0, 0x58 = E4M3 16.0 (:1545-1547)
+  const auto a_h1 = half_fill((size_t)m * max_k, 0x3c00), b_h1 = half_fill((size_t)n * max_k, 0x3c00);
+  const auto a_h8 = half_fill((size_t)m * max_k, 0x4800), b_h8 = half_fill((size_t)n * max_k, 0x4800);
+  const auto a_q1 = byte_fill((size_t)m * max_k / 2, 0x22), b_q1 = byte_fill((size_t)n * max_k / 2, 0x22);
+  const auto a_q6 = byte_fill((size_t)m * max_k / 2, 0x77), b_q6 = byte_fill((size_t)n * max_k / 2, 0x77);
+  const auto a_e1 = byte_fill((size_t)m * max_k, 0x38), b_e1 = byte_fill((size_t)n * max_k, 0x38);
+  const auto a_e16 = byte_fill((size_t)m * max_k, 0x58), b_e16 = byte_fill((size_t)n * max_k, 0x58);
+  Dev c_half(ctx, (size_t)m * n * 2), c_float(ctx, (size_t)m * n * 4);
+
+  struct Path {
+    const char* name;
+    int a_fmt, b_fmt;
+    const Dev* a;
+    const Dev* b;
+    double product;
+  };
+  // (first, last) of C for one case
+  auto run_case = [&](const Path& p, int k, bool half) {
+    const Dev& c = half ? c_half : c_float;
+    const size_t bytes = (size_t)m * n * (half ? 2 : 4);
+    check(ctx, mx_memset(ctx, c.p, 0, bytes));
+    check(ctx, mx_accum_gemm(ctx, p.a_fmt, p.a->p, p.b_fmt, p.b->p, c.p, half ? MX_DTYPE_F16 : MX_DTYPE_F32, m,
+                             n, k));
+    if (half) {
+      std::vector<uint16_t> h((size_t)m * n);
+      check(ctx, mx_download(ctx, h.data(), c.p, bytes));
+      return std::make_pair((double)half_to_float(h.front()), (double)half_to_float(h.back()));
+    }
+    std::vector<float> f((size_t)m * n);
+    check(ctx, mx_download(ctx, f.data(), c.p, bytes));
+    return std::make_pair((double)f.front(), (double)f.back());
+  };
+  auto sweep = [&](const Path& p, const std::vector<int>& ks) {
+    std::printf("\n  %s, product per element = %s:\n", p.name, format_value(p.product).c_str());
+    std::printf("    K | exact | half dest C[0] | float dest C[0]\n");
+    for (int k : ks) {
+      const auto hv = run_case(p, k, true);
+      const auto fv = run_case(p, k, false);
+      std::string note;
+      if (!(hv.first == hv.second && fv.first == fv.second))
+        note = "  [non-uniform: half last " + format_value(hv.second) + ", float last " +
+               format_value(fv.second) + "]";
+      std::printf("    %d | %s | %s | %s%s\n", k, format_value(p.product * k).c_str(),
+                  format_value(hv.first).c_str(), format_value(fv.first).c_str(), note.c_str());
+      std::fflush(stdout);
+    }
+  };
+
+  std::printf("\nAccumulator precision/overflow probe (64x128 tile, dot length K):\n");
+  std::printf("  All inputs are constant fills, so every C element has the same exact value.\n");
+  std::printf("  A deviation in 'half dest' but not 'float dest' isolates destination/accumulator precision.\n");
+  const std::vector<int> ones_ks = {1024, 2048, 2080, 4096, 4160, 8192, 16384, 32768, 65504, 65536, 131072};
+  sweep({"half x half -> C, ones", MX_PROBE_F16, MX_PROBE_F16, a_h1.get(), b_h1.get(), 1.0}, ones_ks);
+  sweep({"half x FP4 E2M1 -> C, ones", MX_PROBE_F16, MX_PROBE_FP4, a_h1.get(), b_q1.get(), 1.0}, ones_ks);
+  sweep({"FP4 E2M1 x FP4 E2M1 -> C, ones", MX_PROBE_FP4, MX_PROBE_FP4, a_q1.get(), b_q1.get(), 1.0}, ones_ks);
+  sweep({"FP8 E4M3 x FP8 E4M3 -> C, ones", MX_PROBE_FP8, MX_PROBE_FP8, a_e1.get(), b_e1.get(), 1.0}, ones_ks);
+  std::printf("\n  Overflow cases (products sized to cross half max 65504):\n");
+  sweep({"half x half -> C, 8.0 x 8.0 (product 64)", MX_PROBE_F16, MX_PROBE_F16, a_h8.get(), b_h8.get(), 64.0},
+        {512, 1022, 1024, 2048});
+  sweep({"FP4 E2M1 x FP4 E2M1 -> C, 6.0 x 6.0 (product 36)", MX_PROBE_FP4, MX_PROBE_FP4, a_q6.get(), b_q6.get(),
+         36.0},
+        {1024, 1818, 1820, 2048, 4096});
+  sweep({"FP8 E4M3 x FP8 E4M3 -> C, 16.0 x 16.0 (product 256)", MX_PROBE_FP8, MX_PROBE_FP8, a_e16.get(),
+         b_e16.get(), 256.0},
+        {128, 254, 256, 1024});
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -352,7 +452,7 @@ int main(int argc, char** argv) {
     if (has_flag("--benchmark") || has_flag("--fp4-group-sweep"))
       std::printf("Scalar matmul benchmark: not part of this build.\n");
     if (mlp) run_mlp_benchmark(ctx, tokens, hidden, inter, iterations);
-    if (has_flag("--accum-probe")) std::printf("Accumulator probe: not part of this build.\n");
+    if (has_flag("--accum-probe")) run_accum_probe(ctx);
     if (!kats_ok) fail("One or more packed numeric checks failed.");
     std::printf("PASS\n");
   } catch (const ProbeError& e) {

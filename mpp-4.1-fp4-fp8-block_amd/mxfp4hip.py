@@ -18,6 +18,7 @@ MX_OK, MX_EINVAL, MX_ENODEV, MX_ENOKERNEL, MX_ENOMEM, MX_EGPU = range(6)
 DT_F32, DT_F16, DT_I8, DT_I32, DT_U8 = range(5)
 FMT_FP4_E2M1, FMT_FP8_E4M3, FMT_FP8_E5M2 = range(3)
 MLP_FUSED, MLP_DEQUANT, MLP_W4A4, MLP_REFROW = range(4)
+PROBE_F16, PROBE_FP4, PROBE_FP8 = range(3)
 WFMT_FP8_E4M3, WFMT_FP8_E5M2, WFMT_INT8, WFMT_INT4, WFMT_W8A8 = 1, 2, 3, 4, 5
 
 # Every symbol the header declares (checked by tests/test_abi_exports.py).
@@ -25,7 +26,7 @@ EXPORTS = [
     "mx_create", "mx_destroy", "mx_last_error", "mx_status_string", "mx_device_info",
     "mx_set_stream", "mx_get_stream", "mx_sync", "mx_alloc", "mx_free", "mx_upload",
     "mx_download", "mx_memset", "mx_roundtrip", "mx_pack", "mx_unpack", "mx_mxfp4_quantize",
-    "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_gemm_i8", "mx_swiglu", "mx_mlp_forward",
+    "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_gemm_i8", "mx_accum_gemm", "mx_swiglu", "mx_mlp_forward",
     "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_fmt_quantize", "mx_fmt_mlp_forward",
     "mx_fmt_mlp_benchmark", "mx_fill_normal", "mx_lcg_bytes", "mx_lcg_pattern", "mx_lcg_half",
     "mx_lcg_int8", "mx_checksum_f32", "mx_checksum_i32", "mx_checksum_f16raw",
@@ -89,6 +90,7 @@ def load() -> ctypes.CDLL:
         "mx_mxfp4_matmul": (_int, [_vp, _vp, _int, _vp, _vp, _int, _int, _int, _int, _vp]),
         "mx_gemm_f16": (_int, [_vp, _vp, _int, _vp, _vp, _int, _int, _int]),
         "mx_gemm_i8": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int]),
+        "mx_accum_gemm": (_int, [_vp, _int, _vp, _int, _vp, _vp, _int, _int, _int, _int]),
         "mx_swiglu": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int]),
         "mx_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp, _int,
@@ -236,6 +238,10 @@ class Device:
 
     def gemm_i8(self, a: DevBuf, b: DevBuf, c: DevBuf, m, n, k):
         self._check(load().mx_gemm_i8(self.ctx, a.p, b.p, c.p, m, n, k))
+
+    def accum_gemm(self, a_fmt, a: DevBuf, b_fmt, b: DevBuf, c: DevBuf, c_dtype, m, n, k):
+        """Accumulator-probe GEMM (AccumProbeKernels.metal:41-127)."""
+        self._check(load().mx_accum_gemm(self.ctx, a_fmt, a.p, b_fmt, b.p, c.p, c_dtype, m, n, k))
 
     def swiglu(self, variant, gate: DevBuf, up: DevBuf, mid: DevBuf, tokens, inter):
         self._check(load().mx_swiglu(self.ctx, variant, gate.p, up.p, mid.p, tokens, inter))

@@ -52,3 +52,21 @@ def test_driver_mlp_benchmark_on_gpu():
     assert abs(float(m.group(1)) - 403573) / 403573 < 2e-5
     for row in ("W4A4", "FP8 E5M2 weights", "INT4 weights", "W8A8 MLP", "relative slowdown"):
         assert row in out
+
+
+@needs_driver
+@pytest.mark.gpu
+def test_driver_accum_probe_on_gpu():
+    """--accum-probe (runAccumulatorProbe, main.swift:1523-1713): the table
+    rows behind the reference's published findings (README.md:342-352)."""
+    r = run("--accum-probe", "--skip-tensor", timeout=300)
+    print(r.stdout[-4000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    out = r.stdout
+    assert "Accumulator precision/overflow probe" in out
+    assert "    1818 | 65448 | 65440 | 65448" in out       # one RNE rounding to half
+    assert "    256 | 65536 | inf | 65536" in out          # FP8 x FP8 overflow in half only
+    assert "    131072 | 131072 | inf | 131072" in out    # f32 accumulation, exact
+    assert "    65504 | 65504 | 65504 | 65504" in out
+    assert "non-uniform" not in out
+    assert out.rstrip().endswith("PASS")
