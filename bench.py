@@ -7,7 +7,8 @@ distinct weight sets rotated inside the timed loop (2.2x the 256 MB
 last-level cache, as for MoE experts).  One step = one full MLP forward
 down(silu(gate(x)) * up(x)).
 
-Secondary measurements (configs 0, 1 with T=8, 2, 3 and 4) are reported in
+Secondary measurements (configs 0, 1 with T=8, 2, 3 and 4, and MoE grouped
+experts at the C1 and C2 expert shapes) are reported in
 the same JSON line under "secondary"; they are not the headline value.
 
   value        effective TFLOP/s = 6*T*H*I / (time per step)
@@ -99,6 +100,39 @@ def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt
     return res, (x, sets)
 
 
+def run_moe(dev, M, name, E, per_expert, H, I, iters, warmup, seed):
+    """E experts of shape (H, I), per_expert tokens each, one grouped MoE pass
+    per iteration (mx_moe_benchmark).  Expert weights N(0, 0.02), MXFP4."""
+    counts = [per_expert] * E
+    T = E * per_expert
+    x = dev.alloc(T * H * 2)
+    dev.fill_normal(x, M.DT_F16, T * H, seed, 0.0, 1.0)
+    tmp = dev.alloc(E * I * H * 4)
+    mats = []
+    for j, (n, k) in enumerate(((E * I, H), (E * I, H), (E * H, I))):
+        dev.fill_normal(tmp, M.DT_F32, n * k, seed * 100 + j + 1, 0.0, 0.02)
+        q, sc = dev.alloc(n * k // 2), dev.alloc(n * k // 32)
+        dev.mxfp4_quantize(tmp, M.DT_F32, n, k, q, sc)
+        mats.append((q, sc))
+    tmp.free()
+    w = M.Device.weights(*mats)
+    out = dev.alloc(T * H * 2)
+    secs = dev.moe_benchmark(H, I, counts, x, [w], out, warmup=warmup, iterations=iters, graph=True)
+    us = secs / iters * 1e6
+    wbytes = E * 3 * mxfp4_bytes(I, H)
+    res = {"experts": E, "tokens_per_expert": per_expert, "hidden": H, "intermediate": I, "iters": iters,
+           "us_per_iter": round(us, 3), "tflops": round(6.0 * T * H * I / (us * 1e-6) / 1e12, 3),
+           "weight_bytes": wbytes, "hbm_gbps": round((wbytes + 2 * T * H * 2) / (us * 1e-6) / 1e9, 1)}
+    res["hbm_frac"] = round(res["hbm_gbps"] * 1e9 / HBM_PEAK, 4)
+    for q, sc in mats:
+        q.free()
+        sc.free()
+    x.free()
+    out.free()
+    log(f"[bench] {name}: {us:.2f} us/iter, {res['tflops']} TFLOP/s, {res['hbm_gbps']} GB/s")
+    return res
+
+
 def cpu_baseline(T, H, I, budget_s=12.0):
     """Time the CPU oracle's MLP (f16 activations, MXFP4 weights) on host
     cores, on the same shapes with data generated on the host."""
@@ -166,7 +200,7 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma-separated secondary configs to run (c1_t8,c4,c0,c2,c3); default all")
+                    help="comma-separated secondary configs to run (c1_t8,c4,c0,c2,c3,moe); default all")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only a 256 MiB device-to-device copy x3 (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes) and exit")
@@ -252,6 +286,14 @@ def main():
             wb = 3 * 4096 * 14336 * (0.5 if wfmt == M.WFMT_INT4 else 1)
             r["hbm_frac"] = round(wb / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
             sec[f"c3_{tag}"] = r
+        if want("moe"):
+            # MoE grouped launches at the C1 / C2 expert shapes: 64 experts x 4
+            # tokens (1.5 GB of expert weights per pass) and 8 experts x 512
+            sec["moe_c1_64x4"] = run_moe(dev, M, "MoE C1 shape 64 experts x 4 tokens", 64, 4, 7168, 2048,
+                                         40, 4, seed=8)
+            r = run_moe(dev, M, "MoE C2 shape 8 experts x 512 tokens", 8, 512, 7168, 2048, 20, 2, seed=9)
+            r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
+            sec["moe_c2_8x512"] = r
         result["secondary"] = sec
 
     if not args.no_cpu:

@@ -197,6 +197,28 @@ int mx_mlp_benchmark(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const v
  * (for the per-kernel times); NULL past the last kernel. */
 const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index);
 
+/* ---- MoE grouped experts ------------------------------------------------------ */
+/* No counterpart in the reference (a "next" item of its MXFP4 regime: MoE
+ * experts whose weights are decoded inside the loop).  The MXFP4 MLP of
+ * n_experts experts over one token batch in two grouped launches (gate/up +
+ * SwiGLU for every expert, then down for every expert).
+ *   x     f16 [tokens][hidden], rows grouped by expert: expert e owns the
+ *         counts[e] rows after those of experts 0..e-1 (counts: host array
+ *         of n_experts entries summing to cfg->tokens; 0 is allowed).
+ *   w     experts stacked in the MXFP4 layout, pointers at expert 0: gate and
+ *         up data [E][I][H/2] + scales [E][I][H/32], down data [E][H][I/2] +
+ *         scales [E][H][I/32].
+ *   out   f16 [tokens][hidden], rows in the same order as x.
+ * 1 <= n_experts <= 256.  Experts with at most 16 tokens each take the decode
+ * GEMV (hidden, intermediate % 128); otherwise % 64. */
+int mx_moe_forward(mx_ctx* ctx, const mx_mlp_config* cfg, int n_experts, const int* counts,
+                   const void* x, const mx_mlp_weights* w, void* out);
+/* `iterations` MoE forwards between two HIP events (rotating weight sets), as
+ * mx_mlp_benchmark. */
+int mx_moe_benchmark(mx_ctx* ctx, const mx_mlp_config* cfg, int n_experts, const int* counts,
+                     const void* x, const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
+                     int iterations, int use_graph, double* seconds_out);
+
 /* ---- weight-format rows (config 3) ------------------------------------------ */
 /* Quantize f32 weights [rows][k] into format `wfmt` (scales per the enum). */
 int mx_fmt_quantize(mx_ctx* ctx, int wfmt, const float* w, int rows, int k, void* q,

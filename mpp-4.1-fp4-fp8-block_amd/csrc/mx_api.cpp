@@ -704,6 +704,91 @@ int mx_mlp_benchmark(mx_ctx* c, int variant, const mx_mlp_config* cfg, const voi
   return bench_loop(c, all, warmup, iterations, use_graph, seconds_out, kernel_us_out, n_kernels_out);
 }
 
+// ---- MoE: grouped experts ---------------------------------------------------------
+// Two grouped launches for all experts: the decode GEMV when every expert has
+// at most 16 tokens, else the small-M GEMM family (one tile grid per expert
+// in blockIdx.z).  Expert e owns token rows [off[e], off[e+1]).
+static int build_moe_steps(mx_ctx* c, const mx_mlp_config* cfg, int n_experts, const int* counts,
+                           const void* x, const mx_mlp_weights* w, void* out, std::vector<Step>& steps) {
+  if (int rc = check_mlp_cfg(c, MX_MLP_FUSED, cfg)) return rc;
+  if (n_experts < 1 || n_experts > mx::kMaxGroups)
+    return set_err(c, MX_EINVAL, "MoE needs 1 to %d experts.", mx::kMaxGroups);
+  if (!counts || !x || !w || !out) return set_err(c, MX_EINVAL, "MoE buffers must not be null.");
+  const mx_qmatrix* mats[3] = {&w->gate, &w->up, &w->down};
+  for (const mx_qmatrix* m : mats) {
+    if (!m->data || !m->scales) return set_err(c, MX_EINVAL, "MLP weight buffers must not be null.");
+    if (!aligned16(m->data)) return set_err(c, MX_EINVAL, "MXFP4 weight data must be 16-byte aligned.");
+    if (reinterpret_cast<uintptr_t>(m->scales) & 3u)
+      return set_err(c, MX_EINVAL, "MXFP4 scale planes must be 4-byte aligned.");
+  }
+  if (!aligned16(x) || !aligned16(out))
+    return set_err(c, MX_EINVAL, "Activation and output buffers must be 16-byte aligned.");
+  const int T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
+  mx::GroupTable gu_t{}, dn_t{};
+  long total = 0;
+  int most = 0;
+  for (int e = 0; e < n_experts; e++) {
+    if (counts[e] < 0) return set_err(c, MX_EINVAL, "MoE token counts must not be negative.");
+    gu_t.off[e] = dn_t.off[e] = (int)total;
+    total += counts[e];
+    most = std::max(most, counts[e]);
+  }
+  gu_t.off[n_experts] = dn_t.off[n_experts] = (int)total;
+  if (total != T) return set_err(c, MX_EINVAL, "MoE token counts must add up to tokens (%ld != %d).", total, T);
+  gu_t.b_stride = (size_t)I * H / 2;
+  gu_t.s_stride = (size_t)I * H / 32;
+  dn_t.b_stride = (size_t)H * I / 2;
+  dn_t.s_stride = (size_t)H * I / 32;
+  const size_t mid_b = align_up((size_t)T * I * 2, 256);
+  if (int rc = ensure_ws(c, mid_b)) return rc;
+  uint16_t* mid = static_cast<uint16_t*>(c->ws);
+  hipStream_t st = c->stream;
+  const uint8_t* wg = static_cast<const uint8_t*>(w->gate.data);
+  const uint8_t* sg = static_cast<const uint8_t*>(w->gate.scales);
+  const uint8_t* wu = static_cast<const uint8_t*>(w->up.data);
+  const uint8_t* su = static_cast<const uint8_t*>(w->up.scales);
+  const uint8_t* wd = static_cast<const uint8_t*>(w->down.data);
+  const uint8_t* sd = static_cast<const uint8_t*>(w->down.scales);
+  const int E = n_experts;
+  mx_mlp_config most_cfg = *cfg;
+  most_cfg.tokens = (uint32_t)std::max(most, 1);
+  if (gemv_ok(&most_cfg)) {
+    mx::GemvArgs gu{static_cast<const uint16_t*>(x), wg, sg, wu, su, mid, most, I, H};
+    mx::GemvArgs dn{mid, wd, sd, nullptr, nullptr, static_cast<uint16_t*>(out), most, H, I};
+    steps.push_back({"moe_gemv_gate_up_swiglu", [=] { return mx::launch_gemv_mxfp4_grouped(1, gu, gu_t, E, st); }});
+    steps.push_back({"moe_gemv_down", [=] { return mx::launch_gemv_mxfp4_grouped(0, dn, dn_t, E, st); }});
+    return MX_OK;
+  }
+  if (!mx::gemm_q_ok(mx::AK_F16, mx::BK_MXFP4, mx::EPI_SWIGLU_F16, most, I, H) ||
+      !mx::gemm_q_ok(mx::AK_F16, mx::BK_MXFP4, mx::EPI_STORE_F16, most, H, I))
+    return set_err(c, MX_EINVAL, "MoE experts with more than 16 tokens need hidden and intermediate %% 64 == 0.");
+  mx::QGemmArgs gu{x, nullptr, wg, sg, wu, su, mid, nullptr, most, I, H, 0};
+  mx::QGemmArgs dn{mid, nullptr, wd, sd, nullptr, nullptr, out, nullptr, most, H, I, 0};
+  steps.push_back({"moe_gemm_q_gate_up_swiglu",
+                   [=] { return mx::launch_gemm_q_grouped(mx::EPI_SWIGLU_F16, gu, gu_t, E, st); }});
+  steps.push_back({"moe_gemm_q_down", [=] { return mx::launch_gemm_q_grouped(mx::EPI_STORE_F16, dn, dn_t, E, st); }});
+  return MX_OK;
+}
+
+int mx_moe_forward(mx_ctx* c, const mx_mlp_config* cfg, int n_experts, const int* counts, const void* x,
+                   const mx_mlp_weights* w, void* out) {
+  if (!c) return MX_EINVAL;
+  std::vector<Step> steps;
+  if (int rc = build_moe_steps(c, cfg, n_experts, counts, x, w, out, steps)) return rc;
+  return run_steps(c, steps);
+}
+
+int mx_moe_benchmark(mx_ctx* c, const mx_mlp_config* cfg, int n_experts, const int* counts, const void* x,
+                     const mx_mlp_weights* sets, int n_sets, void* out, int warmup, int iterations, int use_graph,
+                     double* seconds_out) {
+  if (!c) return MX_EINVAL;
+  if (!sets || n_sets <= 0) return set_err(c, MX_EINVAL, "benchmark needs at least one weight set.");
+  std::vector<std::vector<Step>> all((size_t)n_sets);
+  for (int i = 0; i < n_sets; i++)
+    if (int rc = build_moe_steps(c, cfg, n_experts, counts, x, &sets[i], out, all[i])) return rc;
+  return bench_loop(c, all, warmup, iterations, use_graph, seconds_out, nullptr, nullptr);
+}
+
 // ---- weight formats ---------------------------------------------------------------
 int mx_fmt_quantize(mx_ctx* c, int wfmt, const float* w, int rows, int k, void* q, void* scales) {
   if (!c) return MX_EINVAL;

@@ -167,10 +167,36 @@ __device__ __forceinline__ float scaled(float acc, const QGemmArgs& g, const flo
   return v;
 }
 
+constexpr int out_bytes(int epi) {
+  return epi == EPI_STORE_F32 || epi == EPI_STORE_I32 || epi == EPI_SWIGLU_F32 ? 4 : 2;
+}
+
+struct NoGroups {};
+
 // NWB: 32-column weight blocks per wave (2: 128 weight rows per tile, 1: 64).
-template <int AK, int BK, int EPI, int NWB>
-__global__ __launch_bounds__(256, 2) void k_gemm_q(QGemmArgs g) {
+// GROUPED (MoE): blockIdx.z is the group; group e owns rows [off[e],
+// off[e+1]) of A and C and its weights / scales sit e * stride bytes after
+// group 0's; g.tiles_m covers the largest group and tiles past a group's
+// rows exit at once.  Grouped launches do not split K.
+template <int AK, int BK, int EPI, int NWB, bool GROUPED>
+__global__ __launch_bounds__(256, 2) void k_gemm_q(
+    QGemmArgs g, typename std::conditional<GROUPED, GroupTable, NoGroups>::type grp) {
   constexpr bool DUAL = is_dual(EPI);
+  if constexpr (GROUPED) {
+    const int e = blockIdx.z;
+    const int t0 = grp.off[e], rows = grp.off[e + 1] - t0;
+    if ((int)(blockIdx.x % g.tiles_m) * kTM >= rows) return;  // workgroup-uniform, before any barrier
+    g.m = rows;
+    g.a = reinterpret_cast<const uint8_t*>(g.a) + (size_t)t0 * g.k * (AK == AK_F32 ? 4 : AK == AK_F16 ? 2 : 1);
+    if (AK == AK_I8) g.a_scale += t0;
+    g.c = reinterpret_cast<uint8_t*>(g.c) + (size_t)t0 * g.n * out_bytes(EPI);
+    g.b0 = reinterpret_cast<const uint8_t*>(g.b0) + e * grp.b_stride;
+    g.s0 = reinterpret_cast<const uint8_t*>(g.s0) + e * grp.s_stride;
+    if (DUAL) {
+      g.b1 = reinterpret_cast<const uint8_t*>(g.b1) + e * grp.b_stride;
+      g.s1 = reinterpret_cast<const uint8_t*>(g.s1) + e * grp.s_stride;
+    }
+  }
   constexpr int KS = AInfo<AK>::KS;
   constexpr int RA = AInfo<AK>::RB;          // A bytes per row per stage
   constexpr int RB = b_row_bytes<BK>(KS);    // B bytes per row per stage
@@ -467,7 +493,8 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   QGemmArgs g = g0;
   g.tiles_m = (g.m + kTM - 1) / kTM;
   const int tiles_n = is_dual(EPI) ? g.n / 64 : g.n / (NWB * 64);
-  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g);
+  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g,
+                     NoGroups{});
   if (splits > 1) {
     const size_t n = (size_t)g.m * g.n;
     hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, splits);
@@ -482,6 +509,17 @@ hipError_t launch_wn(const QGemmArgs& g, int splits, hipStream_t st) {
 }
 
 int stage_k(int ak) { return ak == AK_I8 ? 128 : 64; }
+
+// Grouped launch: g.m = the largest group's rows.
+template <int AK, int BK, int EPI, int NWB>
+hipError_t launch_q_grouped(const QGemmArgs& g0, const GroupTable& gt, int groups, hipStream_t st) {
+  QGemmArgs g = g0;
+  g.tiles_m = (g.m + kTM - 1) / kTM;
+  const int tiles_n = is_dual(EPI) ? g.n / 64 : g.n / (NWB * 64);
+  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true>), dim3(g.tiles_m * tiles_n, 1, groups), dim3(256), 0, st, g,
+                     gt);
+  return hipGetLastError();
+}
 
 }  // namespace qgemm
 
@@ -518,6 +556,18 @@ bool gemm_q_ok(int ak, int bk, int epi, int m, int n, int k) {
     case EPI_SWIGLU_HALF: return launch_wn<AK, BK, EPI_SWIGLU_HALF>(g, s, st);                      \
     default: return hipErrorInvalidValue;                                                           \
   }
+
+// MoE form: MXFP4 weights, f16 activations, SwiGLU (mid f16) or f16 store.
+hipError_t launch_gemm_q_grouped(int epi, const QGemmArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
+  if (groups < 1 || groups > kMaxGroups || !gemm_q_ok(AK_F16, BK_MXFP4, epi, g.m, g.n, g.k)) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_SWIGLU_F16: return launch_q_grouped<AK_F16, BK_MXFP4, EPI_SWIGLU_F16, 2>(g, gt, groups, st);
+    case EPI_STORE_F16:
+      return g.n % 128 == 0 ? launch_q_grouped<AK_F16, BK_MXFP4, EPI_STORE_F16, 2>(g, gt, groups, st)
+                            : launch_q_grouped<AK_F16, BK_MXFP4, EPI_STORE_F16, 1>(g, gt, groups, st);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_gemm_q(int ak, int bk, int epi, const QGemmArgs& g, hipStream_t st) {
   if (!gemm_q_ok(ak, bk, epi, g.m, g.n, g.k)) return hipErrorInvalidValue;

@@ -40,7 +40,7 @@ namespace mx {
 constexpr int kStepK = 128;   // K per lane step: 4 lane groups x 32-element blocks
 // NSTEP: steps per wave whose weight loads are issued together (2, 4 or 8).
 constexpr int kW = 8;         // waves per workgroup
-constexpr int kMaxScaleRegs = 4;  // scale dwords staged per thread: K <= 16384
+constexpr int kMaxScaleRegs = 4;  // scale dwords staged per thread: K <= 16384 / row groups
 
 // 16-byte global -> LDS DMA of one lane (LDS base wave-uniform).
 __device__ __forceinline__ void dma16(const void* src, void* lds) {
@@ -52,40 +52,48 @@ constexpr int gemv_wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4
 
 // Dynamic LDS layout: [scales 16 rows x K/32 bytes][x T rows x (K+8) halves]
 // [reduction W x 16 x 17 floats].
-__host__ __device__ inline size_t gemv_lds_bytes(int t, int k) {
-  const size_t s = (size_t)16 * (k / 32);
+__host__ __device__ inline size_t gemv_lds_bytes(int t, int k, int ng = 1) {
+  const size_t s = (size_t)16 * ng * (k / 32);
   const size_t xs = (size_t)t * (k + 8) * 2;
   return ((s + 15) / 16) * 16 + ((xs + 15) / 16) * 16 + (size_t)kW * 16 * 17 * 4;
 }
 
-template <bool DUAL, int NSTEP>
-__global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+// One workgroup: NG = kW / WPG row groups g0 .. g0+NG-1 (row group g =
+// weight rows 16g .. 16g+15, or gate / up channels 8g .. 8g+7) over all of
+// K; WPG waves share each group's K steps.  More groups per workgroup stage
+// x once for more rows (the activations are T x K, as large as 16 rows of
+// weights at T = 4).
+template <bool DUAL, int NSTEP, int WPG>
+__device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* lds) {
+  constexpr int NG = kW / WPG;
+  static_assert(NG * WPG == kW && NG <= 2, "row groups per workgroup");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gi = wave / WPG, gw = wave % WPG;  // this wave's group and its index in the group
   const int r = lane & 15, lg = lane >> 4;
   const int K = g.k, T = g.t;
   const int S = K / kStepK;
   const int KB = K / 32;
   uint8_t* s_lds = lds;
-  uint16_t* x_lds = reinterpret_cast<uint16_t*>(lds + (((size_t)16 * KB + 15) / 16) * 16);
+  uint16_t* x_lds = reinterpret_cast<uint16_t*>(lds + (((size_t)16 * NG * KB + 15) / 16) * 16);
   float* red = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(x_lds) +
                                         (((size_t)T * (K + 8) * 2 + 15) / 16) * 16);
 
-  // Weight / scale row of tile row `rr`.
-  auto row_ptrs = [&](int rr, const uint8_t*& w, const uint8_t*& s) {
+  // Weight / scale row of workgroup row `wr` (0 .. 16 NG - 1).
+  auto row_ptrs = [&](int wr, const uint8_t*& w, const uint8_t*& s) {
+    const int grp = g0 + wr / 16, rr = wr % 16;
     if (DUAL) {
-      const int c = blockIdx.x * 8 + (rr & 7);
+      const int c = grp * 8 + (rr & 7);
       w = (rr < 8 ? g.b0 : g.b1) + (size_t)c * (K / 2);
       s = (rr < 8 ? g.s0 : g.s1) + (size_t)c * KB;
     } else {
-      const int n = blockIdx.x * 16 + rr;
+      const int n = grp * 16 + rr;
       w = g.b0 + (size_t)n * (K / 2);
       s = g.s0 + (size_t)n * KB;
     }
   };
   const uint8_t* wrow;
   const uint8_t* srow;
-  row_ptrs(r, wrow, srow);
+  row_ptrs(gi * 16 + r, wrow, srow);
   wrow += lg * 16;
 
   // 1) Staging first: x rows go global -> LDS by DMA (no registers), the 16
@@ -101,15 +109,15 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
               reinterpret_cast<uint8_t*>(x_lds) + (size_t)t * (K + 8) * 2 + c * 1024);
     }
   }
-  const int n_sdw = 16 * (KB / 4);  // scale dwords of the 16 rows
+  const int n_sdw = 16 * NG * (KB / 4);  // scale dwords of the workgroup's rows
   uint32_t sreg[kMaxScaleRegs];
 #pragma unroll
   for (int q = 0; q < kMaxScaleRegs; q++) {
     const int i = min(tid + q * 64 * kW, n_sdw - 1);  // clamped: no predicated loads
-    const int rr = i / (KB / 4), c = i % (KB / 4);
+    const int wr = i / (KB / 4), c = i % (KB / 4);
     const uint8_t* w;
     const uint8_t* s;
-    row_ptrs(rr, w, s);
+    row_ptrs(wr, w, s);
     sreg[q] = *reinterpret_cast<const uint32_t*>(s + c * 4);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -118,7 +126,7 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
   uint4 wv[NSTEP];
 #pragma unroll
   for (int b = 0; b < NSTEP; b++) {
-    const int st = min(wave + b * kW, S - 1);  // tail steps re-read a valid step
+    const int st = min(gw + b * WPG, S - 1);  // tail steps re-read a valid step
     const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
     wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     __builtin_amdgcn_sched_barrier(0);
@@ -132,8 +140,8 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
   for (int q = 0; q < kMaxScaleRegs; q++) {
     const int i = tid + q * 64 * kW;
     if (i < n_sdw) {
-      const int rr = i / (KB / 4), c = i % (KB / 4);
-      *reinterpret_cast<uint32_t*>(s_lds + (size_t)rr * KB + c * 4) = sreg[q];
+      const int wr = i / (KB / 4), c = i % (KB / 4);
+      *reinterpret_cast<uint32_t*>(s_lds + (size_t)wr * KB + c * 4) = sreg[q];
     }
   }
   __builtin_amdgcn_s_waitcnt(gemv_wait_vm(NSTEP) & ~(15 << 8));  // + lgkmcnt(0)
@@ -143,13 +151,13 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
   // Lane r feeds activation row r; rows >= T re-read row T-1 (their MFMA rows
   // are never stored), so no load or read is predicated.
   const uint16_t* xr = x_lds + (size_t)(r < T ? r : T - 1) * (K + 8) + lg * 32;
-  const uint8_t* sr = s_lds + (size_t)r * KB + lg;
+  const uint8_t* sr = s_lds + (size_t)(gi * 16 + r) * KB + lg;
   v4f acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
-  for (int s0 = wave; s0 < S; s0 += kW * NSTEP) {
-    if (s0 != wave) {  // later batches (K > 8 steps per wave): load them now
+  for (int s0 = gw; s0 < S; s0 += WPG * NSTEP) {
+    if (s0 != gw) {  // later batches (more than NSTEP steps per wave): load them now
 #pragma unroll
       for (int b = 0; b < NSTEP; b++) {
-        const int st = min(s0 + b * kW, S - 1);
+        const int st = min(s0 + b * WPG, S - 1);
         const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
         wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         __builtin_amdgcn_sched_barrier(0);
@@ -167,11 +175,11 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
     }
 #pragma unroll
     for (int b = 0; b < NSTEP; b++) {
-      const int st = s0 + b * kW;
+      const int st = s0 + b * WPG;
       uint4 xq[4] = {xn[0], xn[1], xn[2], xn[3]};
       const uint32_t sbyte = sn;
       if (b + 1 < NSTEP) {
-        const int stn = min(st + kW, S - 1);
+        const int stn = min(st + WPG, S - 1);
 #pragma unroll
         for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)stn * kStepK + q * 8);
         sn = sr[(size_t)stn * 4];
@@ -193,18 +201,46 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
 #pragma unroll
   for (int v = 0; v < 4; v++) red[(wave * 16 + lg * 4 + v) * 17 + r] = acc0[v] + acc1[v];
   __syncthreads();
-  if (tid < 256) {  // whole waves: thread (token tt, column cc)
-    const int tt = tid >> 4, cc = tid & 15;
+  if (tid < NG * 256) {  // whole waves: thread (group g2, token tt, column cc)
+    const int g2 = tid >> 8, tt = (tid >> 4) & 15, cc = tid & 15;
+    const int grp = g0 + g2;
     float tot = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kW; w++) tot += red[(w * 16 + tt) * 17 + cc];
+    for (int w = 0; w < WPG; w++) tot += red[((g2 * WPG + w) * 16 + tt) * 17 + cc];
     if (DUAL) {
       const float uv = __shfl_xor(tot, 8);  // column cc + 8 is the same channel's up sum
-      if (cc < 8 && tt < T) g.out[(size_t)tt * g.n + blockIdx.x * 8 + cc] = f32_to_f16_bits(silu(tot) * uv);
+      if (cc < 8 && tt < T) g.out[(size_t)tt * g.n + grp * 8 + cc] = f32_to_f16_bits(silu(tot) * uv);
     } else if (tt < T) {
-      g.out[(size_t)tt * g.n + blockIdx.x * 16 + cc] = f32_to_f16_bits(tot);
+      g.out[(size_t)tt * g.n + grp * 16 + cc] = f32_to_f16_bits(tot);
     }
   }
+}
+
+template <bool DUAL, int NSTEP>
+__global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  gemv_body<DUAL, NSTEP, kW>(g, blockIdx.x, lds);
+}
+
+// Grouped (MoE) form: blockIdx.y is the group (expert).  Group e owns token
+// rows [off[e], off[e+1]) of x and out, and its weights sit e * stride bytes
+// after group 0's.  Groups with no tokens exit at once.
+template <bool DUAL, int NSTEP, int WPG>
+__global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4_grouped(GemvArgs g, GroupTable gt) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int e = blockIdx.y;
+  const int t0 = gt.off[e], T = gt.off[e + 1] - t0;
+  if (T <= 0) return;  // workgroup-uniform
+  g.t = T;
+  g.x += (size_t)t0 * g.k;
+  g.out += (size_t)t0 * g.n;
+  g.b0 += e * gt.b_stride;
+  g.s0 += e * gt.s_stride;
+  if (DUAL) {
+    g.b1 += e * gt.b_stride;
+    g.s1 += e * gt.s_stride;
+  }
+  gemv_body<DUAL, NSTEP, WPG>(g, blockIdx.x * (kW / WPG), lds);
 }
 
 template <bool DUAL, int NSTEP>
@@ -235,5 +271,44 @@ hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
 }
 
 size_t gemv_lds_need(int t, int k) { return gemv_lds_bytes(t, k); }
+
+template <bool DUAL, int NSTEP, int WPG>
+static hipError_t launch_grouped_ns(const GemvArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
+  constexpr int NG = kW / WPG;
+  static bool attr_set = false;  // allow up to 160 KB of dynamic LDS (once per instance)
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4_grouped<DUAL, NSTEP, WPG>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int row_groups = DUAL ? g.n / 8 : g.n / 16;
+  hipLaunchKernelGGL((k_gemv_mxfp4_grouped<DUAL, NSTEP, WPG>), dim3(row_groups / NG, groups), dim3(64 * kW),
+                     gemv_lds_bytes(g.t, g.k, NG), st, g, gt);
+  return hipGetLastError();
+}
+
+template <bool DUAL, int WPG>
+static hipError_t launch_grouped_w(const GemvArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
+  const int per_wave = (g.k / kStepK + WPG - 1) / WPG;
+  if (per_wave <= 2) return launch_grouped_ns<DUAL, 2, WPG>(g, gt, groups, st);
+  if (per_wave <= 4) return launch_grouped_ns<DUAL, 4, WPG>(g, gt, groups, st);
+  return launch_grouped_ns<DUAL, 8, WPG>(g, gt, groups, st);
+}
+
+// g.t = the largest group's token count (sizes the LDS); the same
+// preconditions as launch_gemv_mxfp4 for it.  With many workgroups
+// (groups x row groups >= 1024) each workgroup takes two row groups, four
+// waves each, so x is staged once for 32 weight rows.
+hipError_t launch_gemv_mxfp4_grouped(int dual, const GemvArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
+  const int row_groups = dual ? g.n / 8 : g.n / 16;
+  const bool pair = (size_t)groups * row_groups >= 1024 && row_groups % 2 == 0 && g.k <= 8192 &&
+                    gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
+  if (groups < 1 || groups > kMaxGroups || g.t < 1 || g.t > 16 || gemv_lds_bytes(g.t, g.k) > 160 * 1024 ||
+      g.k > 16384 || g.k % kStepK)
+    return hipErrorInvalidValue;
+  if (pair) return dual ? launch_grouped_w<true, kW / 2>(g, gt, groups, st) : launch_grouped_w<false, kW / 2>(g, gt, groups, st);
+  return dual ? launch_grouped_w<true, kW>(g, gt, groups, st) : launch_grouped_w<false, kW>(g, gt, groups, st);
+}
 
 }  // namespace mx

@@ -67,6 +67,14 @@ struct GemmArgs {
 
 hipError_t launch_gemm_h(int bkind, int epi, const GemmArgs& g, hipStream_t st);
 
+// Grouped (MoE) launches: group e owns token rows [off[e], off[e+1]) of the
+// activations / outputs, and its weights (scales) sit e * b_stride
+// (e * s_stride) bytes after group 0's.  Passed by value as a kernel argument.
+constexpr int kMaxGroups = 256;
+struct GroupTable {
+  int off[kMaxGroups + 1];
+  size_t b_stride, s_stride;
+};
 // Small / medium-M GEMM family (mx_gemm_q.hip): 128 x 128 tiles, 64-K
 // stages (128 for W8A8), split K with an ordered reduction for few tiles.
 struct QGemmArgs {
@@ -83,6 +91,9 @@ bool gemm_q_ok(int akind, int bkind, int epi, int m, int n, int k);
 size_t gemm_q_ws_bytes(int akind, int epi, int m, int n, int k);
 int gemm_q_splits(int akind, int epi, int m, int n, int k);
 hipError_t launch_gemm_q(int akind, int bkind, int epi, const QGemmArgs& g, hipStream_t st);
+// Grouped (MoE) form, MXFP4 weights and f16 activations only; g.m = the
+// largest group's rows, epi EPI_SWIGLU_F16 or EPI_STORE_F16, no split K.
+hipError_t launch_gemm_q_grouped(int epi, const QGemmArgs& g, const GroupTable& gt, int groups, hipStream_t st);
 
 // Decode-shaped (tokens <= 16) GEMV (mx_gemv.hip): one workgroup per 16
 // weight rows, K split across its waves and reduced in LDS.
@@ -94,6 +105,9 @@ struct GemvArgs {
   int t, n, k;
 };
 hipError_t launch_gemv_mxfp4(int dual_swiglu, const GemvArgs& g, hipStream_t st);
+
+hipError_t launch_gemv_mxfp4_grouped(int dual_swiglu, const GemvArgs& g, const GroupTable& gt, int groups,
+                                     hipStream_t st);
 
 // Unscaled FP4 x FP4 / FP8 E4M3 x FP8 E4M3 GEMM for the accumulator probe
 // (mx_accum.hip): C f32 or f16 [m][n] = A [m][k] . B [n][k]^T.

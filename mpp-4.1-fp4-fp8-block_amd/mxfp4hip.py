@@ -27,7 +27,8 @@ EXPORTS = [
     "mx_set_stream", "mx_get_stream", "mx_sync", "mx_alloc", "mx_free", "mx_upload",
     "mx_download", "mx_memset", "mx_roundtrip", "mx_pack", "mx_unpack", "mx_mxfp4_quantize",
     "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_gemm_i8", "mx_accum_gemm", "mx_swiglu", "mx_mlp_forward",
-    "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_fmt_quantize", "mx_fmt_mlp_forward",
+    "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_moe_forward", "mx_moe_benchmark",
+    "mx_fmt_quantize", "mx_fmt_mlp_forward",
     "mx_fmt_mlp_benchmark", "mx_fill_normal", "mx_lcg_bytes", "mx_lcg_pattern", "mx_lcg_half",
     "mx_lcg_int8", "mx_checksum_f32", "mx_checksum_i32", "mx_checksum_f16raw",
 ]
@@ -96,6 +97,9 @@ def load() -> ctypes.CDLL:
         "mx_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp, _int,
                                     _int, _int, P(ctypes.c_double), P(ctypes.c_double), P(_int)]),
         "mx_mlp_kernel_name": (ctypes.c_char_p, [_int, ctypes.c_void_p, _int]),
+        "mx_moe_forward": (_int, [_vp, P(MlpConfig), _int, P(_int), _vp, P(MlpWeights), _vp]),
+        "mx_moe_benchmark": (_int, [_vp, P(MlpConfig), _int, P(_int), _vp, P(MlpWeights), _int, _vp,
+                                    _int, _int, _int, P(ctypes.c_double)]),
         "mx_fmt_quantize": (_int, [_vp, _int, _vp, _int, _int, _vp, _vp]),
         "mx_fmt_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_fmt_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp,
@@ -274,6 +278,24 @@ class Device:
             ctypes.byref(nk) if per_kernel else None))
         names = [load().mx_mlp_kernel_name(variant, ctypes.byref(cfg), i).decode() for i in range(nk.value)]
         return secs.value, dict(zip(names, list(kus)[:nk.value]))
+
+    # ---- MoE (experts stacked; x rows grouped by expert) ----
+    def moe_forward(self, hidden, inter, counts, x: DevBuf, w: MlpWeights, out: DevBuf):
+        cfg = MlpConfig(int(sum(counts)), hidden, inter)
+        cnt = (_int * len(counts))(*counts)
+        self._check(load().mx_moe_forward(self.ctx, ctypes.byref(cfg), len(counts), cnt, x.p,
+                                          ctypes.byref(w), out.p))
+
+    def moe_benchmark(self, hidden, inter, counts, x: DevBuf, sets, out: DevBuf, warmup=1,
+                      iterations=20, graph=True):
+        cfg = MlpConfig(int(sum(counts)), hidden, inter)
+        cnt = (_int * len(counts))(*counts)
+        arr = (MlpWeights * len(sets))(*sets)
+        secs = ctypes.c_double()
+        self._check(load().mx_moe_benchmark(self.ctx, ctypes.byref(cfg), len(counts), cnt, x.p, arr,
+                                            len(sets), out.p, warmup, iterations, 1 if graph else 0,
+                                            ctypes.byref(secs)))
+        return secs.value
 
     def fmt_quantize(self, wfmt, w: DevBuf, rows, k, q: DevBuf, scales: DevBuf):
         self._check(load().mx_fmt_quantize(self.ctx, wfmt, w.p, rows, k, q.p, scales.p))
