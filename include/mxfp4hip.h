@@ -219,6 +219,23 @@ int mx_moe_benchmark(mx_ctx* ctx, const mx_mlp_config* cfg, int n_experts, const
                      const void* x, const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
                      int iterations, int use_graph, double* seconds_out);
 
+/* ---- on-disk MXFP4 weights (safetensors) ------------------------------------- */
+/* Locate tensor `name` in a safetensors file (host only: no context, no
+ * device).  dtype string (e.g. "U8"), shape (first max_dims entries), number
+ * of dimensions, file offset and byte size of its data. */
+int mx_safetensors_find(const char* path, const char* name, char* dtype_out, size_t dtype_len,
+                        long long* shape_out, int max_dims, int* ndim_out,
+                        unsigned long long* offset_out, unsigned long long* nbytes_out);
+/* Load MXFP4 weights onto the device with no repack: blocks U8
+ * [..., n, k/32, 16] (or [..., n, k/2]) and scales U8 [..., n, k/32] are the
+ * library's layout (docs/MXFP4-MPP41-GUIDE.md:43-55); leading dimensions are
+ * experts, giving the stacked form mx_moe_forward takes.  out->data and
+ * out->scales are new device buffers (release with mx_free).  count_out =
+ * product of the leading dimensions (1 without), n_out rows, k_out = 32 x
+ * the scale dimension. */
+int mx_load_mxfp4(mx_ctx* ctx, const char* path, const char* blocks_name, const char* scales_name,
+                  mx_qmatrix* out, int* count_out, int* n_out, int* k_out);
+
 /* ---- weight-format rows (config 3) ------------------------------------------ */
 /* Quantize f32 weights [rows][k] into format `wfmt` (scales per the enum). */
 int mx_fmt_quantize(mx_ctx* ctx, int wfmt, const float* w, int rows, int k, void* q,

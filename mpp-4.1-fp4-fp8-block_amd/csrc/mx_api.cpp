@@ -265,6 +265,10 @@ int run_steps(mx_ctx* c, const std::vector<Step>& steps) {
 
 }  // namespace
 
+// Context internals for the other translation units (mx_loader.cpp).
+hipStream_t mx_ctx_stream(mx_ctx* c) { return c->stream; }
+int mx_ctx_error(mx_ctx* c, int code, const char* message) { return set_err(c, code, "%s", message); }
+
 // ===========================================================================
 extern "C" {
 

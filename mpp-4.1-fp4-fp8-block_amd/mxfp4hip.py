@@ -28,10 +28,25 @@ EXPORTS = [
     "mx_download", "mx_memset", "mx_roundtrip", "mx_pack", "mx_unpack", "mx_mxfp4_quantize",
     "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_gemm_i8", "mx_accum_gemm", "mx_swiglu", "mx_mlp_forward",
     "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_moe_forward", "mx_moe_benchmark",
+    "mx_safetensors_find", "mx_load_mxfp4",
     "mx_fmt_quantize", "mx_fmt_mlp_forward",
     "mx_fmt_mlp_benchmark", "mx_fill_normal", "mx_lcg_bytes", "mx_lcg_pattern", "mx_lcg_half",
     "mx_lcg_int8", "mx_checksum_f32", "mx_checksum_i32", "mx_checksum_f16raw",
 ]
+
+
+def safetensors_find(path, name):
+    """(dtype, shape, file offset, byte size) of a tensor in a safetensors
+    file, from the library's own header reader (no device needed)."""
+    dt = ctypes.create_string_buffer(16)
+    shape = (ctypes.c_longlong * 8)()
+    nd = ctypes.c_int()
+    off, nb = ctypes.c_ulonglong(), ctypes.c_ulonglong()
+    rc = load().mx_safetensors_find(str(path).encode(), name.encode(), dt, 16, shape, 8, ctypes.byref(nd),
+                                    ctypes.byref(off), ctypes.byref(nb))
+    if rc:
+        raise MxError(rc, f"tensor {name} not found or file unreadable")
+    return dt.value.decode(), list(shape[:nd.value]), off.value, nb.value
 
 
 class MxError(RuntimeError):
@@ -98,6 +113,11 @@ def load() -> ctypes.CDLL:
                                     _int, _int, P(ctypes.c_double), P(ctypes.c_double), P(_int)]),
         "mx_mlp_kernel_name": (ctypes.c_char_p, [_int, ctypes.c_void_p, _int]),
         "mx_moe_forward": (_int, [_vp, P(MlpConfig), _int, P(_int), _vp, P(MlpWeights), _vp]),
+        "mx_safetensors_find": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _sz,
+                                       P(ctypes.c_longlong), _int, P(_int), P(ctypes.c_ulonglong),
+                                       P(ctypes.c_ulonglong)]),
+        "mx_load_mxfp4": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, P(QMatrix),
+                                 P(_int), P(_int), P(_int)]),
         "mx_moe_benchmark": (_int, [_vp, P(MlpConfig), _int, P(_int), _vp, P(MlpWeights), _int, _vp,
                                     _int, _int, _int, P(ctypes.c_double)]),
         "mx_fmt_quantize": (_int, [_vp, _int, _vp, _int, _int, _vp, _vp]),
@@ -278,6 +298,19 @@ class Device:
             ctypes.byref(nk) if per_kernel else None))
         names = [load().mx_mlp_kernel_name(variant, ctypes.byref(cfg), i).decode() for i in range(nk.value)]
         return secs.value, dict(zip(names, list(kus)[:nk.value]))
+
+    # ---- on-disk MXFP4 weights ----
+    def load_mxfp4(self, path, blocks_name, scales_name):
+        """(data DevBuf, scales DevBuf, experts, n, k) of a safetensors MXFP4 matrix."""
+        q = QMatrix()
+        cnt, n, k = _int(), _int(), _int()
+        self._check(load().mx_load_mxfp4(self.ctx, str(path).encode(), blocks_name.encode(),
+                                         scales_name.encode(), ctypes.byref(q), ctypes.byref(cnt),
+                                         ctypes.byref(n), ctypes.byref(k)))
+        data = DevBuf(self, q.data, cnt.value * n.value * k.value // 2)
+        scales = DevBuf(self, q.scales, cnt.value * n.value * k.value // 32)
+        self._bufs.update((data, scales))
+        return data, scales, cnt.value, n.value, k.value
 
     # ---- MoE (experts stacked; x rows grouped by expert) ----
     def moe_forward(self, hidden, inter, counts, x: DevBuf, w: MlpWeights, out: DevBuf):
