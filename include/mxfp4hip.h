@@ -108,6 +108,11 @@ int mx_device_info(mx_ctx* ctx, char* name_out, size_t name_len, int* cu_count, 
 int mx_set_stream(mx_ctx* ctx, void* stream);
 void* mx_get_stream(mx_ctx* ctx);
 int mx_sync(mx_ctx* ctx);
+/* Device time of the work enqueued between the two calls on the context's
+ * stream (HIP events; the counterpart of a command buffer's gpuStartTime /
+ * gpuEndTime, main.swift:1761-1779).  mx_timer_stop waits for that work. */
+int mx_timer_start(mx_ctx* ctx);
+int mx_timer_stop(mx_ctx* ctx, double* seconds_out);
 
 /* ---- device memory (device.makeBuffer, main.swift:219, 640-917) --------- */
 int mx_alloc(mx_ctx* ctx, size_t bytes, void** dptr);
@@ -152,15 +157,19 @@ int mx_gemm_f16(mx_ctx* ctx, const void* a, int a_dtype, const void* b, float* c
  * mpp_mlp_i8_i8_i32_n128 (MPPMLPKernels.metal:61-70), the W8A8 core.
  * n % 64 == 0, k % 128 == 0. */
 int mx_gemm_i8(mx_ctx* ctx, const int8_t* a, const int8_t* b, int32_t* c, int m, int n, int k);
-/* Accumulator-probe GEMM: the accum_{h_h,h_fp4,fp4_fp4,fp8_fp8}_{h,f}
- * family (AccumProbeKernels.metal:41-127; ABI a, b, c, m, n, k).
+/* Typed probe GEMM: the accumulator-probe family accum_{h_h,h_fp4,fp4_fp4,
+ * fp8_fp8}_{h,f} (AccumProbeKernels.metal:41-127) and the scalar benchmark
+ * matmuls half_int4_matmul_half / int8_half_matmul_half /
+ * int4_int8_matmul (PackedNumericKernels.metal:246-423); ABI a, b, c, m, n, k.
  * C[m][n] = sum_k A[m][k] * B[n][k], A [m][k] and B [n][k] K-contiguous in
- * format a_fmt / b_fmt (MX_PROBE_*; FP4 is E2M1 two per byte, low nibble =
- * even k; FP4 and FP8 carry no scales); f32 accumulation; C f32 or f16
- * (c_dtype; f16 is one RNE rounding of the f32 sum, >= 65520 -> inf).
- * Pairs: (F16, F16), (F16, FP4), (FP4, FP4), (FP8, FP8).  Any k >= 1 (even
- * with FP4); n % 64 == 0; FP4 / FP8 A also needs m % 32 == 0. */
-enum { MX_PROBE_F16 = 0, MX_PROBE_FP4 = 1, MX_PROBE_FP8 = 2 };
+ * format a_fmt / b_fmt (MX_PROBE_*: FP4 = E2M1 and INT4 = signed
+ * ((b & 15) ^ 8) - 8, both two per byte, low nibble = even k, no scales;
+ * FP8 = E4M3; I8 = int8); f32 accumulation (i32 for INT4 x INT4); C f32 or
+ * f16 (c_dtype; f16 is one RNE rounding of the f32 sum, >= 65520 -> inf), i32
+ * for INT4 x INT4.  Pairs: (F16, F16), (F16, FP4), (FP4, FP4), (FP8, FP8),
+ * (F16, INT4), (I8, F16), (INT4, INT4).  Any k >= 1 (even with 4-bit
+ * operands); n % 64 == 0; FP4 / FP8 A also needs m % 32 == 0. */
+enum { MX_PROBE_F16 = 0, MX_PROBE_FP4 = 1, MX_PROBE_FP8 = 2, MX_PROBE_INT4 = 3, MX_PROBE_I8 = 4 };
 int mx_accum_gemm(mx_ctx* ctx, int a_fmt, const void* a, int b_fmt, const void* b, void* c,
                   int c_dtype, int m, int n, int k);
 /* SwiGLU: variant 0 mpp_mlp_swiglu_float, 1 mpp_mlp_swiglu_half,

@@ -89,6 +89,58 @@ hipError_t launch_pad_rows(const uint8_t* src, size_t rows, size_t rb, uint8_t* 
   return hipGetLastError();
 }
 
+// Exact widening with the same zero padding: signed INT4 (two per byte, low
+// nibble first, ((b & 15) ^ 8) - 8, PackedNumericKernels.metal:25-28) or
+// INT8 rows of k values -> rows of kp values, as int8 (INT4 only) or f16.
+template <bool SRC_I4, bool DST_F16>
+__global__ void k_widen_rows(const uint8_t* src, size_t rows, size_t k, void* dst, size_t kp) {
+  const size_t total = rows * kp;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / kp, j = i % kp;
+    int v = 0;
+    if (j < k) {
+      if (SRC_I4) {
+        const uint8_t b = src[r * (k / 2) + j / 2];
+        v = ((int)((j & 1) ? b >> 4 : b & 15) ^ 8) - 8;
+      } else {
+        v = (int)(int8_t)src[r * k + j];
+      }
+    }
+    if (DST_F16) reinterpret_cast<uint16_t*>(dst)[i] = f32_to_f16_bits((float)v);
+    else reinterpret_cast<int8_t*>(dst)[i] = (int8_t)v;
+  }
+}
+
+hipError_t launch_widen_rows(int src_int4, int dst_f16, const uint8_t* src, size_t rows, size_t k, void* dst,
+                             size_t kp, hipStream_t st) {
+  if (k > kp || (src_int4 && k % 2)) return hipErrorInvalidValue;
+  size_t blocks = (rows * kp + 255) / 256;
+  blocks = blocks < 1 ? 1 : blocks > 4096 ? 4096 : blocks;  // grid-stride loop covers the rest
+  const dim3 grid((unsigned)blocks), block(256);
+  if (src_int4) {
+    if (dst_f16) hipLaunchKernelGGL((k_widen_rows<true, true>), grid, block, 0, st, src, rows, k, dst, kp);
+    else hipLaunchKernelGGL((k_widen_rows<true, false>), grid, block, 0, st, src, rows, k, dst, kp);
+  } else {
+    if (dst_f16) hipLaunchKernelGGL((k_widen_rows<false, true>), grid, block, 0, st, src, rows, k, dst, kp);
+    else hipLaunchKernelGGL((k_widen_rows<false, false>), grid, block, 0, st, src, rows, k, dst, kp);
+  }
+  return hipGetLastError();
+}
+
+// dst[0, n) = value (16-bit), same purpose as k_fill_u8.
+__global__ void k_fill_u16(uint16_t* dst, size_t n, uint32_t value) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = (uint16_t)value;
+}
+
+hipError_t launch_fill_u16(uint16_t* dst, size_t n, uint16_t value, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  size_t blocks = (n + 255) / 256;
+  blocks = blocks < 1 ? 1 : blocks > 1024 ? 1024 : blocks;
+  hipLaunchKernelGGL(k_fill_u16, dim3((unsigned)blocks), dim3(256), 0, st, dst, n, (uint32_t)value);
+  return hipGetLastError();
+}
+
 // dst[0, n) = value, for planes a caller's graph capture may record (a fill
 // kernel rather than a memset node).
 __global__ void k_fill_u8(uint8_t* dst, size_t n, uint32_t value) {

@@ -26,6 +26,7 @@ struct mx_ctx {
   // scratch owned by the context (grown on demand)
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  hipEvent_t t0 = nullptr, t1 = nullptr;  // mx_timer_start / mx_timer_stop
 };
 
 namespace {
@@ -313,6 +314,8 @@ void mx_destroy(mx_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   if (c->ws) (void)hipFree(c->ws);
+  if (c->t0) (void)hipEventDestroy(c->t0);
+  if (c->t1) (void)hipEventDestroy(c->t1);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -334,6 +337,25 @@ int mx_set_stream(mx_ctx* c, void* stream) {
 }
 
 void* mx_get_stream(mx_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+
+int mx_timer_start(mx_ctx* c) {
+  if (!c) return MX_EINVAL;
+  if (!c->t0) MX_HIP(c, hipEventCreate(&c->t0));
+  if (!c->t1) MX_HIP(c, hipEventCreate(&c->t1));
+  MX_HIP(c, hipEventRecord(c->t0, c->stream));
+  return MX_OK;
+}
+
+int mx_timer_stop(mx_ctx* c, double* seconds_out) {
+  if (!c || !seconds_out) return MX_EINVAL;
+  if (!c->t0) return set_err(c, MX_EINVAL, "mx_timer_stop without mx_timer_start.");
+  MX_HIP(c, hipEventRecord(c->t1, c->stream));
+  MX_HIP(c, hipEventSynchronize(c->t1));
+  float ms = 0.0f;
+  MX_HIP(c, hipEventElapsedTime(&ms, c->t0, c->t1));
+  *seconds_out = ms / 1000.0;
+  return MX_OK;
+}
 
 int mx_sync(mx_ctx* c) {
   if (!c) return MX_EINVAL;
@@ -525,51 +547,77 @@ int mx_accum_gemm(mx_ctx* c, int a_fmt, const void* a, int b_fmt, const void* b,
   const bool hh = a_fmt == MX_PROBE_F16 && b_fmt == MX_PROBE_F16;
   const bool hq = a_fmt == MX_PROBE_F16 && b_fmt == MX_PROBE_FP4;
   const bool qq = (a_fmt == MX_PROBE_FP4 && b_fmt == MX_PROBE_FP4) || (a_fmt == MX_PROBE_FP8 && b_fmt == MX_PROBE_FP8);
-  if (!hh && !hq && !qq) return set_err(c, MX_EINVAL, "Unsupported probe operand pair (%d, %d).", a_fmt, b_fmt);
+  const bool h4 = a_fmt == MX_PROBE_F16 && b_fmt == MX_PROBE_INT4;
+  const bool i8h = a_fmt == MX_PROBE_I8 && b_fmt == MX_PROBE_F16;
+  const bool i44 = a_fmt == MX_PROBE_INT4 && b_fmt == MX_PROBE_INT4;
+  if (!hh && !hq && !qq && !h4 && !i8h && !i44)
+    return set_err(c, MX_EINVAL, "Unsupported probe operand pair (%d, %d).", a_fmt, b_fmt);
   if (m <= 0 || n <= 0 || k <= 0) return set_err(c, MX_EINVAL, "matmul sizes must be positive.");
   if (n % 64) return set_err(c, MX_EINVAL, "matmul n must be a multiple of 64.");
   if (qq && m % 32) return set_err(c, MX_EINVAL, "FP4 / FP8 probe matmul needs m %% 32 == 0.");
-  if ((a_fmt == MX_PROBE_FP4 || b_fmt == MX_PROBE_FP4) && k % 2)
-    return set_err(c, MX_EINVAL, "packed FP4 rows need an even k.");
+  auto nibbles = [](int f) { return f == MX_PROBE_FP4 || f == MX_PROBE_INT4; };
+  if ((nibbles(a_fmt) || nibbles(b_fmt)) && k % 2)
+    return set_err(c, MX_EINVAL, "packed 4-bit rows need an even k.");
   if (!a || !b || !out || !aligned16(a) || !aligned16(b) || !aligned16(out))
     return set_err(c, MX_EINVAL, "matmul buffers must be non-null and 16-byte aligned.");
-  if (c_dtype != MX_DTYPE_F32 && c_dtype != MX_DTYPE_F16)
-    return set_err(c, MX_EINVAL, "probe C must be f32 or f16.");
-  const int epi = c_dtype == MX_DTYPE_F32 ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
-  // Workspace: [A padded][B padded][unit scale plane][split-K partials].  K
-  // is padded with zero codes to a multiple of 64 (the reference takes any
-  // dot length, e.g. 1022 or 1818), sized once so nothing moves in between.
-  auto row_bytes = [](int fmt, size_t kk) { return fmt == MX_PROBE_F16 ? kk * 2 : fmt == MX_PROBE_FP8 ? kk : kk / 2; };
-  const size_t kp = align_up((size_t)k, 64);
+  if (i44 ? c_dtype != MX_DTYPE_I32 : (c_dtype != MX_DTYPE_F32 && c_dtype != MX_DTYPE_F16))
+    return set_err(c, MX_EINVAL, i44 ? "INT4 x INT4 probe C must be i32." : "probe C must be f32 or f16.");
+  const int epi = i44 ? mx::EPI_STORE_I32 : c_dtype == MX_DTYPE_F32 ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
+  // Workspace: [A'][B'][unit scale plane][split-K partials], sized once so
+  // nothing moves in between.  K is padded with zeros to the GEMM's stage
+  // (64; 128 for int8) since the reference takes any dot length (e.g. 1022,
+  // 1818); INT8 A is widened to f16 and INT4 x INT4 to int8, both exactly.
+  auto row_bytes = [](int fmt, size_t kk) {
+    return fmt == MX_PROBE_F16 ? kk * 2 : (fmt == MX_PROBE_FP8 || fmt == MX_PROBE_I8) ? kk : kk / 2;
+  };
+  const size_t kp = align_up((size_t)k, i44 ? 128 : 64);
   const bool pad = kp != (size_t)k;
-  const size_t a_sz = pad ? align_up((size_t)m * row_bytes(a_fmt, kp), 256) : 0;
-  const size_t b_sz = pad ? align_up((size_t)n * row_bytes(b_fmt, kp), 256) : 0;
-  const size_t plane = hq ? align_up((size_t)n * (kp / 32), 256) : 0;
-  const int bk = hq ? mx::BK_MXFP4 : mx::BK_F16;
-  const size_t part = (hh || hq) && mx::gemm_q_ok(mx::AK_F16, bk, epi, m, n, (int)kp)
-                          ? mx::gemm_q_ws_bytes(mx::AK_F16, epi, m, n, (int)kp) : 0;
+  const size_t a_sz = i8h ? align_up((size_t)m * kp * 2, 256) : i44 ? align_up((size_t)m * kp, 256)
+                      : pad ? align_up((size_t)m * row_bytes(a_fmt, kp), 256) : 0;
+  const size_t b_sz = i44 ? align_up((size_t)n * kp, 256) : pad ? align_up((size_t)n * row_bytes(b_fmt, kp), 256) : 0;
+  const size_t plane = hq ? align_up((size_t)n * (kp / 32), 256) : h4 ? align_up((size_t)n * (kp / 32) * 2, 256) : 0;
+  const int ak = i44 ? mx::AK_I8 : mx::AK_F16;
+  const int bk = hq ? mx::BK_MXFP4 : h4 ? mx::BK_INT4G32 : i44 ? mx::BK_I8 : mx::BK_F16;
+  const size_t part = !qq && mx::gemm_q_ok(ak, bk, epi, m, n, (int)kp) ? mx::gemm_q_ws_bytes(ak, epi, m, n, (int)kp) : 0;
   if (int rc = ensure_ws(c, a_sz + b_sz + plane + part)) return rc;
   uint8_t* ws = static_cast<uint8_t*>(c->ws);
+  const uint8_t* ua = static_cast<const uint8_t*>(a);
+  const uint8_t* ub = static_cast<const uint8_t*>(b);
   const void* pa = a;
   const void* pb = b;
-  if (pad) {
-    MX_HIP(c, mx::launch_pad_rows(static_cast<const uint8_t*>(a), m, row_bytes(a_fmt, k), ws,
-                                  row_bytes(a_fmt, kp), c->stream));
-    MX_HIP(c, mx::launch_pad_rows(static_cast<const uint8_t*>(b), n, row_bytes(b_fmt, k), ws + a_sz,
-                                  row_bytes(b_fmt, kp), c->stream));
+  hipStream_t st = c->stream;
+  if (i8h || i44) {
+    MX_HIP(c, mx::launch_widen_rows(i44, i8h, ua, m, k, ws, kp, st));
     pa = ws;
+  } else if (pad) {
+    MX_HIP(c, mx::launch_pad_rows(ua, m, row_bytes(a_fmt, k), ws, row_bytes(a_fmt, kp), st));
+    pa = ws;
+  }
+  if (i44) {
+    MX_HIP(c, mx::launch_widen_rows(1, 0, ub, n, k, ws + a_sz, kp, st));
+    pb = ws + a_sz;
+  } else if (pad) {
+    MX_HIP(c, mx::launch_pad_rows(ub, n, row_bytes(b_fmt, k), ws + a_sz, row_bytes(b_fmt, kp), st));
     pb = ws + a_sz;
   }
   if (qq) {
     MX_HIP(c, mx::launch_gemm_f8f6f4_unit(a_fmt == MX_PROBE_FP4, c_dtype == MX_DTYPE_F32,
                                           static_cast<const uint8_t*>(pa), static_cast<const uint8_t*>(pb), out, m,
-                                          n, (int)kp, c->stream));
+                                          n, (int)kp, st));
+    return MX_OK;
+  }
+  if (i44) {  // exact i32 sums of the widened int8 operands
+    mx::QGemmArgs g{pa, nullptr, pb, nullptr, nullptr, nullptr, out, part ? ws + a_sz + b_sz : nullptr, m, n, (int)kp, 0};
+    MX_HIP(c, mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_I32, g, st));
     return MX_OK;
   }
   uint8_t* sc = nullptr;
   if (hq) {  // unscaled FP4 = MXFP4 with every E8M0 byte 127 (1.0)
     sc = ws + a_sz + b_sz;
-    MX_HIP(c, mx::launch_fill_u8(sc, (size_t)n * (kp / 32), 127, c->stream));
+    MX_HIP(c, mx::launch_fill_u8(sc, (size_t)n * (kp / 32), 127, st));
+  } else if (h4) {  // unscaled INT4 = INT4 with every f16 group scale 1.0
+    sc = ws + a_sz + b_sz;
+    MX_HIP(c, mx::launch_fill_u16(reinterpret_cast<uint16_t*>(sc), (size_t)n * (kp / 32), 0x3c00, st));
   }
   return run_gemm(c, pa, MX_DTYPE_F16, bk, pb, sc, out, epi, m, n, (int)kp, a_sz + b_sz + plane);
 }

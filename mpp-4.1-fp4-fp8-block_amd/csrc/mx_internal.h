@@ -114,6 +114,11 @@ hipError_t launch_gemv_mxfp4_grouped(int dual_swiglu, const GemvArgs& g, const G
 bool gemm_f8f6f4_unit_ok(int m, int n, int k);
 // Rows of rb bytes -> rows of rbp >= rb bytes, zero-filled (mx_accum.hip).
 hipError_t launch_pad_rows(const uint8_t* src, size_t rows, size_t rb, uint8_t* dst, size_t rbp, hipStream_t st);
+// INT4 (src_int4) or INT8 rows of k values -> zero-padded rows of kp values
+// as f16 (dst_f16) or int8, exactly (mx_accum.hip).
+hipError_t launch_widen_rows(int src_int4, int dst_f16, const uint8_t* src, size_t rows, size_t k, void* dst,
+                             size_t kp, hipStream_t st);
+hipError_t launch_fill_u16(uint16_t* dst, size_t n, uint16_t value, hipStream_t st);
 // dst[0, n) = value by a kernel (dst 4-byte aligned).
 hipError_t launch_fill_u8(uint8_t* dst, size_t n, uint8_t value, hipStream_t st);
 hipError_t launch_gemm_f8f6f4_unit(int fp4, int out_f32, const uint8_t* a, const uint8_t* b, void* c, int m,

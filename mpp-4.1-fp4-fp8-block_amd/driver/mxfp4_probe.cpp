@@ -12,7 +12,9 @@
 //     (defaults 128, 1024, 4*H, 3 as in :587-590)
 //   --accum-probe         accumulator precision / overflow probe
 //                         (runAccumulatorProbe, :1523-1713)
-//   --benchmark, --fp4-group-sweep: reported as not built
+//   --benchmark           big matmul rows (runBigMatmulBenchmark, :380-584)
+//     --matmul-size=S --m= --n= --k= --iterations= (defaults 2048, 3);
+//     --fp4-group-sweep adds the g8 rows
 //   success ends with "PASS"; a failure prints "error: <message>" on stderr
 //   and exits 1 (:83-88).
 //
@@ -320,6 +322,95 @@ void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long i
   print_slowdowns(rows);
 }
 
+// ---- big matmul benchmark ---------------------------------------------------
+// runBigMatmulBenchmark (main.swift:380-584): the reference's scalar
+// one-thread-per-output matmul rows, here on the matrix cores through
+// mx_accum_gemm, with the reference's data generators, timing span (device
+// time of `iterations` back-to-back matmuls, :1761-1779) and checksums.
+// --fp4-group-sweep adds the g8 rows; the unpack group width is a property of
+// Metal's packed_numeric decode, and on MI355X FP4 feeds the matrix cores
+// directly, so g8 and g16 rows run the same path.
+
+std::string format_mib(size_t bytes) {  // formatBytes (:2894-2897)
+  char buf[64];
+  std::snprintf(buf, sizeof buf, "%.2f MiB", bytes / (1024.0 * 1024.0));
+  return buf;
+}
+
+void run_matmul_benchmark(mx_ctx* ctx, long rows, long columns, long depth, long iterations, bool sweep) {
+  const size_t R = rows, C = columns, D = depth;
+  std::printf("\nBig packed matmul benchmark:\n");
+  std::printf("  shape: A %ldx%ld, B %ldx%ld, C %ldx%ld\n", rows, depth, depth, columns, rows, columns);
+  std::printf("  packed A bytes: %s, packed B^T bytes: %s\n", format_mib(R * D / 2).c_str(), format_mib(C * D / 2).c_str());
+  std::printf("  half A bytes: %s\n", format_mib(R * D * 2).c_str());
+  std::printf("  iterations: %ld\n", iterations);
+  if (sweep) std::printf("  FP4 unpack group sweep: 8 and 16 elements\n");
+
+  // Reference inputs (:408-412).
+  std::vector<uint8_t> a_bytes(R * D / 2), b_bytes(C * D / 2);
+  std::vector<uint16_t> a_half(R * D), b_half(C * D);
+  std::vector<int8_t> a_i8(R * D);
+  mx_lcg_bytes(0x12345678u, a_bytes.size(), a_bytes.data());
+  mx_lcg_bytes(0x87654321u, b_bytes.size(), b_bytes.data());
+  mx_lcg_half(0x2468ace0u, a_half.size(), 0.25f, a_half.data());
+  mx_lcg_int8(0x13579bdfu, a_i8.size(), a_i8.data());
+  mx_lcg_half(0xfdb97531u, b_half.size(), 0.03125f, b_half.data());
+  Dev a(ctx, a_bytes.size()), b(ctx, b_bytes.size()), ah(ctx, a_half.size() * 2), bh(ctx, b_half.size() * 2),
+      a8(ctx, a_i8.size()), out(ctx, R * C * 4);
+  check(ctx, mx_upload(ctx, a.p, a_bytes.data(), a_bytes.size()));
+  check(ctx, mx_upload(ctx, b.p, b_bytes.data(), b_bytes.size()));
+  check(ctx, mx_upload(ctx, ah.p, a_half.data(), a_half.size() * 2));
+  check(ctx, mx_upload(ctx, bh.p, b_half.data(), b_half.size() * 2));
+  check(ctx, mx_upload(ctx, a8.p, a_i8.data(), a_i8.size()));
+
+  enum Sum { SUM_F32, SUM_F16RAW, SUM_I32 };
+  std::vector<RowResult> rows_out;
+  auto run_row = [&](const char* name, int a_fmt, const Dev& pa, int b_fmt, const Dev& pb, int c_dtype, Sum sum) {
+    const int m = (int)rows, n = (int)columns, k = (int)depth;
+    check(ctx, mx_accum_gemm(ctx, a_fmt, pa.p, b_fmt, pb.p, out.p, c_dtype, m, n, k));  // warm-up
+    check(ctx, mx_memset(ctx, out.p, 0, R * C * 4));
+    double secs = 0.0;
+    check(ctx, mx_timer_start(ctx));
+    for (long i = 0; i < iterations; i++) check(ctx, mx_accum_gemm(ctx, a_fmt, pa.p, b_fmt, pb.p, out.p, c_dtype, m, n, k));
+    check(ctx, mx_timer_stop(ctx, &secs));
+    std::string cs;
+    char buf[96];
+    int samples = 0;
+    if (sum == SUM_F32) {
+      cs = checksum(ctx, out.p, R * C, false);
+    } else if (sum == SUM_F16RAW) {
+      std::vector<uint16_t> h(R * C);
+      check(ctx, mx_download(ctx, h.data(), out.p, h.size() * 2));
+      const unsigned long long v = mx_checksum_f16raw(h.data(), h.size(), &samples);
+      std::snprintf(buf, sizeof buf, "raw16 sum %llu over %d samples", v, samples);
+      cs = buf;
+    } else {
+      std::vector<int32_t> h(R * C);
+      check(ctx, mx_download(ctx, h.data(), out.p, h.size() * 4));
+      const long long v = mx_checksum_i32(h.data(), h.size(), &samples);
+      std::snprintf(buf, sizeof buf, "%lld over %d samples", v, samples);
+      cs = buf;
+    }
+    rows_out.push_back({name, secs, (int)iterations, cs});
+  };
+  run_row("FP4 E2M1 g16 -> FP32 accumulate", MX_PROBE_FP4, a, MX_PROBE_FP4, b, MX_DTYPE_F32, SUM_F32);
+  if (sweep) run_row("FP4 E2M1 g8 -> FP32 accumulate", MX_PROBE_FP4, a, MX_PROBE_FP4, b, MX_DTYPE_F32, SUM_F32);
+  run_row("half x FP4 E2M1 g16 -> half accumulate", MX_PROBE_F16, ah, MX_PROBE_FP4, b, MX_DTYPE_F16, SUM_F16RAW);
+  if (sweep)
+    run_row("half x FP4 E2M1 g8 -> half accumulate", MX_PROBE_F16, ah, MX_PROBE_FP4, b, MX_DTYPE_F16, SUM_F16RAW);
+  run_row("half x INT4 -> half accumulate", MX_PROBE_F16, ah, MX_PROBE_INT4, b, MX_DTYPE_F16, SUM_F16RAW);
+  run_row("INT8 x half -> half accumulate", MX_PROBE_I8, a8, MX_PROBE_F16, bh, MX_DTYPE_F16, SUM_F16RAW);
+  run_row("INT4 x INT4 -> INT32 accumulate", MX_PROBE_INT4, a, MX_PROBE_INT4, b, MX_DTYPE_I32, SUM_I32);
+  for (const RowResult& r : rows_out) {  // printMatmulBenchmarkResult (:2754-2761)
+    const double tops = 2.0 * R * C * D * r.iterations / r.seconds / 1e12;
+    std::printf("  %s:\n", r.name.c_str());
+    std::printf("    %.3f ms/matmul, %.3f effective TOPS\n", r.seconds * 1000.0 / r.iterations, tops);
+    std::printf("    checksum: %s\n", r.checksum.c_str());
+  }
+  print_slowdowns(rows_out);
+  std::fflush(stdout);
+}
+
 // ---- accumulator precision / overflow probe -------------------------------
 // runAccumulatorProbe (main.swift:1523-1713): constant-fill 64 x 128 GEMMs of
 // dot length K with a half and a float destination, for half x half,
@@ -426,6 +517,14 @@ int main(int argc, char** argv) {
     // Argument checks of runMLPBenchmark (:592-597), done before the device
     // is opened so that a bad command line fails the same way everywhere.
     const bool mlp = has_flag("--mlp-benchmark");
+    const bool bench = has_flag("--benchmark");
+    const long msize = int_argument("--matmul-size", 2048);
+    const long mm = int_argument("--m", msize), mn = int_argument("--n", msize), mk = int_argument("--k", msize);
+    const long miters = int_argument("--iterations", 3);
+    if (bench) {  // runBigMatmulBenchmark's checks (:387-392)
+      if (mm <= 0 || mn <= 0 || mk <= 0 || miters <= 0) fail("Matmul sizes and iterations must be positive.");
+      if (mk % 16) fail("Matmul K/depth must be a multiple of 16 for packed FP4 groups.");
+    }
     const long tokens = int_argument("--mlp-tokens", 128);
     const long hidden = int_argument("--mlp-hidden", 1024);
     const long inter = int_argument("--mlp-intermediate", hidden * 4);
@@ -449,8 +548,7 @@ int main(int argc, char** argv) {
     const bool kats_ok = run_kats(ctx);
     if (has_flag("--skip-tensor")) std::printf("Tensor creation probe: skipped by --skip-tensor.\n");
     else std::printf("Tensor creation probe: not applicable (no tensor objects on ROCm).\n");
-    if (has_flag("--benchmark") || has_flag("--fp4-group-sweep"))
-      std::printf("Scalar matmul benchmark: not part of this build.\n");
+    if (bench) run_matmul_benchmark(ctx, mm, mn, mk, miters, has_flag("--fp4-group-sweep"));
     if (mlp) run_mlp_benchmark(ctx, tokens, hidden, inter, iterations);
     if (has_flag("--accum-probe")) run_accum_probe(ctx);
     if (!kats_ok) fail("One or more packed numeric checks failed.");

@@ -18,13 +18,13 @@ MX_OK, MX_EINVAL, MX_ENODEV, MX_ENOKERNEL, MX_ENOMEM, MX_EGPU = range(6)
 DT_F32, DT_F16, DT_I8, DT_I32, DT_U8 = range(5)
 FMT_FP4_E2M1, FMT_FP8_E4M3, FMT_FP8_E5M2 = range(3)
 MLP_FUSED, MLP_DEQUANT, MLP_W4A4, MLP_REFROW = range(4)
-PROBE_F16, PROBE_FP4, PROBE_FP8 = range(3)
+PROBE_F16, PROBE_FP4, PROBE_FP8, PROBE_INT4, PROBE_I8 = range(5)
 WFMT_FP8_E4M3, WFMT_FP8_E5M2, WFMT_INT8, WFMT_INT4, WFMT_W8A8 = 1, 2, 3, 4, 5
 
 # Every symbol the header declares (checked by tests/test_abi_exports.py).
 EXPORTS = [
     "mx_create", "mx_destroy", "mx_last_error", "mx_status_string", "mx_device_info",
-    "mx_set_stream", "mx_get_stream", "mx_sync", "mx_alloc", "mx_free", "mx_upload",
+    "mx_set_stream", "mx_get_stream", "mx_sync", "mx_timer_start", "mx_timer_stop", "mx_alloc", "mx_free", "mx_upload",
     "mx_download", "mx_memset", "mx_roundtrip", "mx_pack", "mx_unpack", "mx_mxfp4_quantize",
     "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_gemm_i8", "mx_accum_gemm", "mx_swiglu", "mx_mlp_forward",
     "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_moe_forward", "mx_moe_benchmark",
@@ -93,6 +93,8 @@ def load() -> ctypes.CDLL:
         "mx_set_stream": (_int, [_vp, _vp]),
         "mx_get_stream": (_vp, [_vp]),
         "mx_sync": (_int, [_vp]),
+        "mx_timer_start": (_int, [_vp]),
+        "mx_timer_stop": (_int, [_vp, P(ctypes.c_double)]),
         "mx_alloc": (_int, [_vp, _sz, P(_vp)]),
         "mx_free": (_int, [_vp, _vp]),
         "mx_upload": (_int, [_vp, _vp, _vp, _sz]),
@@ -227,6 +229,14 @@ class Device:
 
     def sync(self):
         self._check(load().mx_sync(self.ctx))
+
+    def timer_start(self):
+        self._check(load().mx_timer_start(self.ctx))
+
+    def timer_stop(self) -> float:
+        secs = ctypes.c_double()
+        self._check(load().mx_timer_stop(self.ctx, ctypes.byref(secs)))
+        return secs.value
 
     # ---- codecs ----
     def roundtrip(self, fmt: int, values) -> tuple[np.ndarray, np.ndarray]:

@@ -25,6 +25,9 @@ def run(*args, timeout=120):
      "MLP hidden and intermediate sizes must be multiples of 16 for packed FP4 weights."),
     (["--mlp-benchmark", "--mlp-tokens=0"], "MLP sizes and iterations must be positive."),
     (["--mlp-benchmark", "--mlp-iterations=-2"], "MLP sizes and iterations must be positive."),
+    (["--benchmark", "--k=100"], "Matmul K/depth must be a multiple of 16 for packed FP4 groups."),
+    (["--benchmark", "--m=0"], "Matmul sizes and iterations must be positive."),
+    (["--benchmark", "--iterations=-1"], "Matmul sizes and iterations must be positive."),
 ])
 def test_driver_rejects_bad_arguments(args, message):
     # checked before the device is opened (main.swift:592-597), so this runs anywhere
@@ -69,4 +72,39 @@ def test_driver_accum_probe_on_gpu():
     assert "    131072 | 131072 | inf | 131072" in out    # f32 accumulation, exact
     assert "    65504 | 65504 | 65504 | 65504" in out
     assert "non-uniform" not in out
+    assert out.rstrip().endswith("PASS")
+
+
+@needs_driver
+@pytest.mark.gpu
+def test_driver_matmul_benchmark_on_gpu():
+    """--benchmark --fp4-group-sweep (runBigMatmulBenchmark, main.swift:380-584)
+    at 256^3 on the reference's LCG data; the INT4 x INT4 row is exact integer
+    arithmetic, so its checksum is pinned by numpy on the same bytes."""
+    import numpy as np
+    import oracle as O
+    s = 256
+    r = run("--benchmark", "--fp4-group-sweep", f"--matmul-size={s}", "--iterations=2", "--skip-tensor", timeout=300)
+    print(r.stdout[-4000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    out = r.stdout
+    for row in ("FP4 E2M1 g16 -> FP32 accumulate", "FP4 E2M1 g8 -> FP32 accumulate",
+                "half x FP4 E2M1 g16 -> half accumulate", "half x FP4 E2M1 g8 -> half accumulate",
+                "half x INT4 -> half accumulate", "INT8 x half -> half accumulate",
+                "INT4 x INT4 -> INT32 accumulate", "relative slowdown"):
+        assert row in out, row
+    a = O.lcg_bytes(0x12345678, s * s // 2).reshape(s, s // 2)
+    b = O.lcg_bytes(0x87654321, s * s // 2).reshape(s, s // 2)
+
+    def i4(x):
+        x = x.astype(np.int64)
+        v = np.empty((x.shape[0], x.shape[1] * 2), np.int64)
+        v[:, 0::2], v[:, 1::2] = ((x & 15) ^ 8) - 8, ((x >> 4) ^ 8) - 8
+        return v
+
+    c = (i4(a) @ i4(b).T).reshape(-1)
+    step = max(1, c.size // 32)
+    want = f"{int(c[::step].sum())} over {len(c[::step])} samples"
+    m = re.search(r"INT4 x INT4 -> INT32 accumulate:\n.*\n\s+checksum: (.*)", out)
+    assert m and m.group(1).strip() == want, (m and m.group(1), want)
     assert out.rstrip().endswith("PASS")

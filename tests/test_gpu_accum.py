@@ -175,3 +175,49 @@ def test_accum_gemm_half_paths_random(dev, k):
         b.free()
         c.free()
     a.free()
+
+
+def _int4(b):
+    """Signed INT4 codes, low nibble = even k (PackedNumericKernels.metal:25-28)."""
+    lo, hi = (b & 15).astype(np.int64), (b >> 4).astype(np.int64)
+    out = np.empty(b.shape[:-1] + (b.shape[-1] * 2,), np.int64)
+    out[..., 0::2], out[..., 1::2] = (lo ^ 8) - 8, (hi ^ 8) - 8
+    return out
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 128, 256), (48, 64, 1022), (32, 192, 130)])
+def test_int_pairs(dev, m, n, k):
+    """half x INT4 and INT8 x half against float64; INT4 x INT4 exact i32."""
+    rng = np.random.default_rng(m * n + k)
+    a16 = (rng.standard_normal((m, k)) * 0.25).astype(np.float16)
+    a8 = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    a4 = rng.integers(0, 256, (m, k // 2), dtype=np.uint8)
+    b4 = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    b16 = (rng.standard_normal((n, k)) * 0.03).astype(np.float16)
+    bufs = {name: dev.upload(arr) for name, arr in
+            (("a16", a16), ("a8", a8), ("a4", a4), ("b4", b4), ("b16", b16))}
+    c = dev.alloc(m * n * 4)
+    cases = [(M.PROBE_F16, "a16", M.PROBE_INT4, "b4", a16.astype(np.float64) @ _int4(b4).T.astype(np.float64)),
+             (M.PROBE_I8, "a8", M.PROBE_F16, "b16", a8.astype(np.float64) @ b16.astype(np.float64).T)]
+    for a_fmt, a_name, b_fmt, b_name, ref in cases:
+        dev.accum_gemm(a_fmt, bufs[a_name], b_fmt, bufs[b_name], c, M.DT_F32, m, n, k)
+        got = dev.download(c, np.float32, (m, n)).astype(np.float64)
+        assert np.abs(got - ref).max() <= 1e-5 * (np.abs(ref).max() + 1), (a_fmt, b_fmt, m, n, k)
+    dev.accum_gemm(M.PROBE_INT4, bufs["a4"], M.PROBE_INT4, bufs["b4"], c, M.DT_I32, m, n, k)
+    got = dev.download(c, np.int32, (m, n)).astype(np.int64)
+    assert np.array_equal(got, _int4(a4) @ _int4(b4).T)
+    with pytest.raises(M.MxError):   # INT4 x INT4 writes i32 only
+        dev.accum_gemm(M.PROBE_INT4, bufs["a4"], M.PROBE_INT4, bufs["b4"], c, M.DT_F32, m, n, k)
+    c.free()
+    for b in bufs.values():
+        b.free()
+
+
+def test_device_timer(dev):
+    dev.timer_start()
+    a, b, c = dev.alloc(64 * 1024 * 2), dev.alloc(128 * 1024 * 2), dev.alloc(64 * 128 * 4)
+    for _ in range(3):
+        dev.accum_gemm(M.PROBE_F16, a, M.PROBE_F16, b, c, M.DT_F32, 64, 128, 1024)
+    assert dev.timer_stop() > 0
+    for x in (a, b, c):
+        x.free()
