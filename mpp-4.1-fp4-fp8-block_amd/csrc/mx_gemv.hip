@@ -216,10 +216,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   }
 }
 
-template <bool DUAL, int NSTEP>
+template <bool DUAL, int NSTEP, int WPG>
 __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  gemv_body<DUAL, NSTEP, kW>(g, blockIdx.x, lds);
+  gemv_body<DUAL, NSTEP, WPG>(g, blockIdx.x * (kW / WPG), lds);
 }
 
 // Grouped (MoE) form: blockIdx.y is the group (expert).  Group e owns token
@@ -243,31 +243,42 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4_grouped(GemvArgs g, Grou
   gemv_body<DUAL, NSTEP, WPG>(g, blockIdx.x * (kW / WPG), lds);
 }
 
-template <bool DUAL, int NSTEP>
-static hipError_t launch_ns(const GemvArgs& g, size_t lds, hipStream_t st) {
+template <bool DUAL, int NSTEP, int WPG>
+static hipError_t launch_ns(const GemvArgs& g, hipStream_t st) {
+  constexpr int NG = kW / WPG;
   static bool attr_set = false;  // allow up to 160 KB of dynamic LDS (once per instance)
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4<DUAL, NSTEP>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4<DUAL, NSTEP, WPG>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const int groups = DUAL ? g.n / 8 : g.n / 16;
-  hipLaunchKernelGGL((k_gemv_mxfp4<DUAL, NSTEP>), dim3(groups), dim3(64 * kW), lds, st, g);
+  const int row_groups = DUAL ? g.n / 8 : g.n / 16;
+  hipLaunchKernelGGL((k_gemv_mxfp4<DUAL, NSTEP, WPG>), dim3(row_groups / NG), dim3(64 * kW),
+                     gemv_lds_bytes(g.t, g.k, NG), st, g);
   return hipGetLastError();
+}
+
+template <bool DUAL, int WPG>
+static hipError_t launch_w(const GemvArgs& g, hipStream_t st) {
+  const int per_wave = (g.k / kStepK + WPG - 1) / WPG;
+  if (per_wave <= 2) return launch_ns<DUAL, 2, WPG>(g, st);
+  if (per_wave <= 4) return launch_ns<DUAL, 4, WPG>(g, st);
+  return launch_ns<DUAL, 8, WPG>(g, st);
 }
 
 // Preconditions (caller): 1 <= t <= 16, n % 16 == 0, k % 128 == 0 and
 // gemv_lds_bytes(t, k) <= 160 KB (checked here).  The batch size is the
 // number of K steps each wave owns (capped at 8), so no wave issues
-// redundant loads when K is short.
+// redundant loads when K is short.  The single (down) GEMV takes two row
+// groups per workgroup when it can (x staged once for 32 rows; measured at
+// C1: 4.6 -> 4.3 us at T = 1, 5.8 -> 5.1 us at T = 8); the dual gate/up GEMV
+// keeps one (its 256 workgroups would halve to 128 and leave CUs idle).
 hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
-  const size_t lds = gemv_lds_bytes(g.t, g.k);
-  if (lds > 160 * 1024 || g.k > 16384 || g.k % kStepK) return hipErrorInvalidValue;
-  const int per_wave = (g.k / kStepK + kW - 1) / kW;
-  if (per_wave <= 2) return dual ? launch_ns<true, 2>(g, lds, st) : launch_ns<false, 2>(g, lds, st);
-  if (per_wave <= 4) return dual ? launch_ns<true, 4>(g, lds, st) : launch_ns<false, 4>(g, lds, st);
-  return dual ? launch_ns<true, 8>(g, lds, st) : launch_ns<false, 8>(g, lds, st);
+  if (gemv_lds_bytes(g.t, g.k) > 160 * 1024 || g.k > 16384 || g.k % kStepK) return hipErrorInvalidValue;
+  const bool pair = !dual && (g.n / 16) % 2 == 0 && g.k <= 8192 && gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
+  if (dual) return launch_w<true, kW>(g, st);
+  return pair ? launch_w<false, kW / 2>(g, st) : launch_w<false, kW>(g, st);
 }
 
 size_t gemv_lds_need(int t, int k) { return gemv_lds_bytes(t, k); }
