@@ -271,12 +271,14 @@ static hipError_t launch_w(const GemvArgs& g, hipStream_t st) {
 // gemv_lds_bytes(t, k) <= 160 KB (checked here).  The batch size is the
 // number of K steps each wave owns (capped at 8), so no wave issues
 // redundant loads when K is short.  The single (down) GEMV takes two row
-// groups per workgroup when it can (x staged once for 32 rows; measured at
-// C1: 4.6 -> 4.3 us at T = 1, 5.8 -> 5.1 us at T = 8); the dual gate/up GEMV
-// keeps one (its 256 workgroups would halve to 128 and leave CUs idle).
+// groups per workgroup from 4 tokens on, where x (T x K) staging is large:
+// x is then staged once for 32 rows (measured at C1 with HBM-cold weights:
+// 5.20 -> 5.11 us at T = 8, but 4.3 -> 4.5 us at T = 1).  The dual gate/up
+// GEMV keeps one group (its 256 workgroups would halve to 128, idling CUs).
 hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
   if (gemv_lds_bytes(g.t, g.k) > 160 * 1024 || g.k > 16384 || g.k % kStepK) return hipErrorInvalidValue;
-  const bool pair = !dual && (g.n / 16) % 2 == 0 && g.k <= 8192 && gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
+  const bool pair = !dual && g.t >= 4 && (g.n / 16) % 2 == 0 && g.k <= 8192 &&
+                    gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
   if (dual) return launch_w<true, kW>(g, st);
   return pair ? launch_w<false, kW / 2>(g, st) : launch_w<false, kW>(g, st);
 }
