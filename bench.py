@@ -200,7 +200,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma-separated secondary configs to run (c1_t8,c4,c0,c2,c3,moe); default all")
+                    help="comma-separated secondary configs to run (c1_t8,c4,c0,c2,c3,moe), or one variant "
+                         "of a config (c0_fused, c2_dequant, c3_int8, ...); default all")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only a 256 MiB device-to-device copy x3 (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes) and exit")
@@ -245,8 +246,8 @@ def main():
         "config": {"workload": "BASELINE configs[1] decode MLP, tokens=1 hidden=7168 "
                                "intermediate=2048, MXFP4 weights, 24 rotated weight sets",
                    "tokens": T, "hidden": H, "intermediate": I, "weight_sets": 24,
-                   "variant": "fused one-launch decode (gate/up and down GEMV workgroups in one "
-                              "grid, in-register FP4 decode, fp16 MFMA)"},
+                   "variant": "decode GEMV, two launches (gate/up + SwiGLU, then down), split-K "
+                              "workgroups, in-register FP4 decode, fp16 MFMA"},
         "mlp_hbm_gbps": round(mlp_bytes / (us * 1e-6) / 1e9, 1),
         "mlp_hbm_frac": round(mlp_bytes / (us * 1e-6) / HBM_PEAK, 4),
         "kernel_us": prim["kernel_us"],
@@ -256,7 +257,7 @@ def main():
     if not args.no_secondary:
         sec = {}
         only = set(t for t in args.only.split(",") if t)
-        want = lambda tag: not only or tag in only
+        want = lambda tag, variant="": not only or tag in only or f"{tag}_{variant}" in only
         if want("c1_t8"):
             r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2)
             b = 3 * mxfp4_bytes(2048, 7168) + 2 * 8 * 7168 * 2 + 2 * 8 * 2048 * 2
@@ -267,20 +268,20 @@ def main():
             r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
             sec["c4_w4a4"] = r
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_W4A4, "w4a4")):
-            if not want("c0"):
-                break
+            if not want("c0", tag):
+                continue
             r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, 24, 100, 10, seed=5)
             sec[f"c0_{tag}"] = r
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant")):
-            if not want("c2"):
-                break
+            if not want("c2", tag):
+                continue
             r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, 24, 100, 10, seed=6)
             r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
             sec[f"c2_{tag}"] = r
         for wfmt, tag in ((M.WFMT_FP8_E4M3, "fp8_e4m3"), (M.WFMT_FP8_E5M2, "fp8_e5m2"),
                           (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32"), (M.WFMT_W8A8, "w8a8")):
-            if not want("c3"):
-                break
+            if not want("c3", tag):
+                continue
             r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, 2, 40, 4, seed=7,
                               wfmt=wfmt)
             wb = 3 * 4096 * 14336 * (0.5 if wfmt == M.WFMT_INT4 else 1)

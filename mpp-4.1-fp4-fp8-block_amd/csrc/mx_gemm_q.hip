@@ -171,8 +171,6 @@ constexpr int out_bytes(int epi) {
   return epi == EPI_STORE_F32 || epi == EPI_STORE_I32 || epi == EPI_SWIGLU_F32 ? 4 : 2;
 }
 
-struct NoGroups {};
-
 // NWB: 32-column weight blocks per wave (2: 128 weight rows per tile, 1: 64).
 // GROUPED (MoE): blockIdx.z is the group; group e owns rows [off[e],
 // off[e+1]) of A and C and its weights / scales sit e * stride bytes after
@@ -180,7 +178,7 @@ struct NoGroups {};
 // rows exit at once.  Grouped launches do not split K.
 template <int AK, int BK, int EPI, int NWB, bool GROUPED>
 __global__ __launch_bounds__(256, 2) void k_gemm_q(
-    QGemmArgs g, typename std::conditional<GROUPED, GroupTable, NoGroups>::type grp) {
+    QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
   constexpr bool DUAL = is_dual(EPI);
   if constexpr (GROUPED) {
     const int e = blockIdx.z;
@@ -493,8 +491,9 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   QGemmArgs g = g0;
   g.tiles_m = (g.m + kTM - 1) / kTM;
   const int tiles_n = is_dual(EPI) ? g.n / 64 : g.n / (NWB * 64);
-  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g,
-                     NoGroups{});
+  // (the ungrouped form's second argument is an unused int: a sized type
+  // keeps the host and device kernel-argument layouts identical)
+  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
   if (splits > 1) {
     const size_t n = (size_t)g.m * g.n;
     hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, splits);
