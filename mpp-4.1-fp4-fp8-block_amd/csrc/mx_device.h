@@ -97,14 +97,6 @@ __device__ __forceinline__ v8h fp4x8_dequant_f16(uint32_t src, uint32_t sb) {
   return h;
 }
 
-// Same, with the byte-255 check hoisted: `any255` is a wave-uniform flag
-// (ballot over the wave's scale bytes), so the common path has no
-// divergent branch per decode.
-__device__ __forceinline__ v8h fp4x8_dequant_f16_u(uint32_t src, uint32_t sb, bool any255) {
-  if (__builtin_expect(!any255, 1)) return fp4x8_to_f16x8(src, e8m0_as_cvt_scale(sb));
-  return fp4x8_dequant_f16(src, sb);
-}
-
 // Block amax -> E8M0 scale byte (BASELINE quantizer:
 // 2^(floor(log2(amax)) - 2)).  `amax_bits` = max of |x| bit patterns.
 // Non-finite -> 255, zero -> 127, exponents below -127 clamp to byte 0.

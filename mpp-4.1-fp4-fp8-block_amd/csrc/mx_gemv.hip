@@ -32,6 +32,8 @@
 // costs (an empty kernel costs ~2.5 us back to back, a pure 14.7 MB read
 // ~4 us); cross-workgroup synchronisation is far worse (an agent-scope grid
 // barrier costs ~14 us), so gate/up and down stay two plain launches.
+#include <type_traits>
+
 #include "mx_device.h"
 #include "mx_internal.h"
 
@@ -148,58 +150,79 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
+  // E8M0 byte 255 (+inf to the reference, NaN to the hardware) takes an
+  // exact slow decode.  One scan of the workgroup's staged scales decides,
+  // so the common loop below carries no per-step check or branch.
+  bool any255;
+  {
+    const int nbytes = 16 * NG * KB;  // a multiple of 64: K % 128 == 0
+    uint32_t hit = 0;
+    for (int i = lane * 16; i < nbytes; i += 64 * 16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(s_lds + i);
+      const uint32_t d[4] = {~v.x, ~v.y, ~v.z, ~v.w};  // a 0xff byte becomes a zero byte
+#pragma unroll
+      for (int j = 0; j < 4; j++) hit |= (d[j] - 0x01010101u) & ~d[j] & 0x80808080u;
+    }
+    any255 = __ballot(hit != 0) != 0;
+  }
+
   // Lane r feeds activation row r; rows >= T re-read row T-1 (their MFMA rows
-  // are never stored), so no load or read is predicated.
+  // are never stored), so no load or read is predicated.  Four accumulators
+  // (one per 32-K slice of a step) keep four independent MFMA chains.
   const uint16_t* xr = x_lds + (size_t)(r < T ? r : T - 1) * (K + 8) + lg * 32;
   const uint8_t* sr = s_lds + (size_t)(gi * 16 + r) * KB + lg;
-  v4f acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
-  for (int s0 = gw; s0 < S; s0 += WPG * NSTEP) {
-    if (s0 != gw) {  // later batches (more than NSTEP steps per wave): load them now
+  v4f acc[4] = {};
+  auto steps = [&](auto slow_tag) {
+    constexpr bool SLOW = decltype(slow_tag)::value;
+    for (int s0 = gw; s0 < S; s0 += WPG * NSTEP) {
+      if (s0 != gw) {  // later batches (more than NSTEP steps per wave): load them now
+#pragma unroll
+        for (int b = 0; b < NSTEP; b++) {
+          const int st = min(s0 + b * WPG, S - 1);
+          const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
+          wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // LDS operands are read one step ahead of their MFMAs so that LDS
+      // latency overlaps the previous step's decode and MFMAs.
+      uint4 xn[4];
+      uint32_t sn;
+      {
+        const int st = min(s0, S - 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)st * kStepK + q * 8);
+        sn = sr[(size_t)st * 4];
+      }
 #pragma unroll
       for (int b = 0; b < NSTEP; b++) {
-        const int st = min(s0 + b * WPG, S - 1);
-        const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
-        wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    // LDS operands are read one step ahead of their MFMAs so that LDS
-    // latency overlaps the previous step's decode and MFMAs.
-    uint4 xn[4];
-    uint32_t sn;
-    {
-      const int st = min(s0, S - 1);
+        const int st = s0 + b * WPG;
+        uint4 xq[4] = {xn[0], xn[1], xn[2], xn[3]};
+        const uint32_t sbyte = sn;
+        if (b + 1 < NSTEP) {
+          const int stn = min(st + WPG, S - 1);
 #pragma unroll
-      for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)st * kStepK + q * 8);
-      sn = sr[(size_t)st * 4];
-    }
+          for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)stn * kStepK + q * 8);
+          sn = sr[(size_t)stn * 4];
+        }
+        if (st < S) {  // wave-uniform; no global loads inside
+          const uint32_t wd[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
+          const float scale = e8m0_as_cvt_scale(sbyte);
 #pragma unroll
-    for (int b = 0; b < NSTEP; b++) {
-      const int st = s0 + b * WPG;
-      uint4 xq[4] = {xn[0], xn[1], xn[2], xn[3]};
-      const uint32_t sbyte = sn;
-      if (b + 1 < NSTEP) {
-        const int stn = min(st + WPG, S - 1);
-#pragma unroll
-        for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)stn * kStepK + q * 8);
-        sn = sr[(size_t)stn * 4];
-      }
-      if (st < S) {  // wave-uniform; no global loads inside
-        const bool any255 = __ballot(sbyte == 255u) != 0;
-        const uint32_t wd[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const v8h bq = fp4x8_dequant_f16_u(wd[q], sbyte, any255);
-          if (q & 1) acc1 = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq[q]), bq, acc1);
-          else acc0 = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq[q]), bq, acc0);
+          for (int q = 0; q < 4; q++) {
+            const v8h bq = SLOW ? fp4x8_dequant_f16(wd[q], sbyte) : fp4x8_to_f16x8(wd[q], scale);
+            acc[q] = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq[q]), bq, acc[q]);
+          }
         }
       }
     }
-  }
+  };
+  if (__builtin_expect(any255, 0)) steps(std::true_type{});
+  else steps(std::false_type{});
 
   // acc element v: token (lane/16)*4 + v, column (weight row) lane % 16.
 #pragma unroll
-  for (int v = 0; v < 4; v++) red[(wave * 16 + lg * 4 + v) * 17 + r] = acc0[v] + acc1[v];
+  for (int v = 0; v < 4; v++) red[(wave * 16 + lg * 4 + v) * 17 + r] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
   __syncthreads();
   if (tid < NG * 256) {  // whole waves: thread (group g2, token tt, column cc)
     const int g2 = tid >> 8, tt = (tid >> 4) & 15, cc = tid & 15;

@@ -220,6 +220,34 @@ def test_decode_gemv_shapes(dev, T, H, I):
     d.free()
 
 
+@pytest.mark.parametrize("T,which", [(1, "down"), (5, "down"), (1, "gate"), (3, "up")])
+def test_decode_e8m0_255(dev, T, which):
+    """E8M0 byte 255 is +inf to the reference (bits << 23), NaN to the
+    hardware's scaled convert: the GEMV decodes a workgroup holding one
+    exactly, so NaN and +-inf land where the oracle's do and the finite
+    outputs stay within tolerance.  A byte-0 block (2^-127) rides along."""
+    H, I = 512, 1024
+    d = MlpData(dev, T, H, I, seed=91 + T)
+    q, s, n, k = d.mats[{"gate": 0, "up": 1, "down": 2}[which]]
+    sc = dev.download(s, np.uint8, (n, k // 32))
+    sc[3, 2] = 255
+    sc[n - 1, :] = 255
+    sc[100, 0] = 0
+    dev.upload(sc, s)
+    got = run_mlp(dev, d, M.MLP_FUSED).astype(np.float64)
+    ref = oracle_mlp(d, M.MLP_FUSED)
+    assert np.isnan(ref).any()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    if which == "down":  # columns 3 and H-1 are non-finite, the rest are not
+        assert fin.sum() == T * (H - 2)
+        rel, cos = O.mlp_error(got[fin], ref[fin])
+        assert rel <= TOL and cos >= COS, (rel, cos)
+    d.free()
+
+
 def test_decode_back_to_back_distinct_inputs(dev):
     """Consecutive forwards with different inputs share the context's mid
     buffer; enqueued back to back, each must produce its own result."""

@@ -103,8 +103,10 @@ def test_moe_gemm_experts(dev, counts, H, I):
 
 def test_moe_one_expert_is_the_decode_mlp(dev):
     """One expert through the grouped GEMV runs the same arithmetic as the
-    ungrouped decode GEMV: bit-identical to mx_mlp_forward."""
-    T, H, I = 5, 512, 1024
+    ungrouped decode GEMV: bit-identical to mx_mlp_forward.  T = 3 keeps
+    both launchers on the same K split (the ungrouped down GEMV pairs row
+    groups from 4 tokens on, the grouped one from 1024 workgroups on)."""
+    T, H, I = 3, 512, 1024
     d = MlpData(dev, T, H, I, seed=61)
     out = dev.alloc(T * H * 2)
     dev.moe_forward(H, I, [T], d.x, d.weights, out)
