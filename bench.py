@@ -211,7 +211,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(the MXFP4 MLP hot path is a single-GPU kernel; see DESIGN.md for how it shards).",
+              "(the MXFP4 MLP hot path here is a single-GPU kernel; a multi-GPU run would shard "
+              "the weight rows across GPUs).",
               file=sys.stderr)
         sys.exit(2)
 

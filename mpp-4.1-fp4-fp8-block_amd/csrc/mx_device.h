@@ -76,25 +76,27 @@ __device__ __forceinline__ v8h fp4x8_to_f16x8(uint32_t src, float scale) {
   return r;
 }
 
+// 8 FP4 codes times an infinite scale, as halves: +-0 codes give NaN
+// (0 * inf), every other code +-inf.
+__device__ __forceinline__ v8h fp4x8_times_inf_f16(uint32_t src) {
+  v8h h;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const uint32_t nib = (src >> (4 * e)) & 15u;
+    const uint32_t bits = (nib & 7u) ? ((nib & 8u) ? 0xfc00u : 0x7c00u) : 0x7e00u;
+    h[e] = __builtin_bit_cast(_Float16, (uint16_t)bits);
+  }
+  return h;
+}
+
 // Dequantize 8 FP4 codes with E8M0 byte `sb` using the reference's scale
 // semantics (bits << 23).  Bytes 0..254 take the single-instruction path
 // (the hardware reads byte 0 as 2^-127, which gives the same halves as the
 // reference's 0.0 because 6 * 2^-127 underflows f16).  Byte 255 is +inf in
-// the reference but NaN to the hardware, so it takes an exact slow path.
+// the reference but NaN to the hardware, so it is formed from the codes.
 __device__ __forceinline__ v8h fp4x8_dequant_f16(uint32_t src, uint32_t sb) {
   if (__builtin_expect(sb != 255u, 1)) return fp4x8_to_f16x8(src, e8m0_as_cvt_scale(sb));
-  const float inf = e8m0_to_float(255u);
-  v2f f[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 0),
-              __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 1),
-              __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 2),
-              __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(src, 1.0f, 3)};
-  v8h h;
-#pragma unroll
-  for (int t = 0; t < 4; t++) {
-    h[2 * t] = (_Float16)(f[t][0] * inf);
-    h[2 * t + 1] = (_Float16)(f[t][1] * inf);
-  }
-  return h;
+  return fp4x8_times_inf_f16(src);
 }
 
 // Block amax -> E8M0 scale byte (BASELINE quantizer:

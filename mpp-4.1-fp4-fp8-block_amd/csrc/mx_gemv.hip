@@ -32,8 +32,6 @@
 // costs (an empty kernel costs ~2.5 us back to back, a pure 14.7 MB read
 // ~4 us); cross-workgroup synchronisation is far worse (an agent-scope grid
 // barrier costs ~14 us), so gate/up and down stay two plain launches.
-#include <type_traits>
-
 #include "mx_device.h"
 #include "mx_internal.h"
 
@@ -150,9 +148,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
-  // E8M0 byte 255 (+inf to the reference, NaN to the hardware) takes an
-  // exact slow decode.  One scan of the workgroup's staged scales decides,
-  // so the common loop below carries no per-step check or branch.
+  // E8M0 byte 255 (+inf to the reference, NaN to the hardware) needs an
+  // exact decode.  One scan of the workgroup's staged scales decides, so
+  // the common loop carries no per-step check or branch.
   bool any255;
   {
     const int nbytes = 16 * NG * KB;  // a multiple of 64: K % 128 == 0
@@ -172,8 +170,21 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   const uint16_t* xr = x_lds + (size_t)(r < T ? r : T - 1) * (K + 8) + lg * 32;
   const uint8_t* sr = s_lds + (size_t)(gi * 16 + r) * KB + lg;
   v4f acc[4] = {};
-  auto steps = [&](auto slow_tag) {
-    constexpr bool SLOW = decltype(slow_tag)::value;
+  if (__builtin_expect(any255, 0)) {
+    // Rare: one step at a time, weights re-read (the batch above is left in
+    // flight), so this path holds few registers next to the unrolled one.
+#pragma nounroll
+    for (int st = gw; st < S; st += WPG) {
+      const uint4 w = *reinterpret_cast<const uint4*>(wrow + (size_t)st * 64);
+      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+      const uint32_t sbyte = sr[(size_t)st * 4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 xq = *reinterpret_cast<const uint4*>(xr + (size_t)st * kStepK + q * 8);
+        acc[q] = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq), fp4x8_dequant_f16(wd[q], sbyte), acc[q]);
+      }
+    }
+  } else {
     for (int s0 = gw; s0 < S; s0 += WPG * NSTEP) {
       if (s0 != gw) {  // later batches (more than NSTEP steps per wave): load them now
 #pragma unroll
@@ -209,16 +220,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
           const uint32_t wd[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
           const float scale = e8m0_as_cvt_scale(sbyte);
 #pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const v8h bq = SLOW ? fp4x8_dequant_f16(wd[q], sbyte) : fp4x8_to_f16x8(wd[q], scale);
-            acc[q] = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq[q]), bq, acc[q]);
-          }
+          for (int q = 0; q < 4; q++)
+            acc[q] = mfma_f16_16x16x32(__builtin_bit_cast(v8h, xq[q]), fp4x8_to_f16x8(wd[q], scale), acc[q]);
         }
       }
     }
-  };
-  if (__builtin_expect(any255, 0)) steps(std::true_type{});
-  else steps(std::false_type{});
+  }
 
   // acc element v: token (lane/16)*4 + v, column (weight row) lane % 16.
 #pragma unroll
