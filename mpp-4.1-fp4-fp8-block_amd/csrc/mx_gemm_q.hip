@@ -176,7 +176,11 @@ constexpr int out_bytes(int epi) {
 // off[e+1]) of A and C and its weights / scales sit e * stride bytes after
 // group 0's; g.tiles_m covers the largest group and tiles past a group's
 // rows exit at once.  Grouped launches do not split K.
-template <int AK, int BK, int EPI, int NWB, bool GROUPED>
+// BCH: K stages per B DMA chunk.  A 4-bit weight row holds 32 bytes per
+// 64-K stage and an 8-bit one 64; B is staged BCH stages at a time (4 and 2)
+// so that every DMA moves whole 128-byte lines (8 rows per instruction), the
+// fastest LDS-DMA pattern.  BCH = 1 stages B per stage.
+template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH>
 __global__ __launch_bounds__(256, 2) void k_gemm_q(
     QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
   constexpr bool DUAL = is_dual(EPI);
@@ -199,18 +203,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
   constexpr int RA = AInfo<AK>::RB;          // A bytes per row per stage
   constexpr int RB = b_row_bytes<BK>(KS);    // B bytes per row per stage
   constexpr int TBR = NWB * 64;               // weight rows per tile
+  constexpr int RBC = RB * BCH;              // B bytes per row per chunk
   constexpr int NA = kTM * RA / 1024 / 4;    // A DMA instructions per wave per stage
-  constexpr int NBW = TBR * RB / 1024;       // B DMA instructions per stage (all waves)
-  constexpr int NB = NBW >= 4 ? NBW / 4 : 1; // per wave (waves >= NBW issue none)
+  constexpr int NBC = TBR * RBC / 1024;      // B DMA instructions per chunk (all waves)
+  constexpr int NB = NBC >= 4 ? NBC / 4 : 1; // per wave (waves >= NBC issue none)
   constexpr bool SCALES4 = BK == BK_MXFP4 || BK == BK_INT4G32;
   constexpr int KSTEPS = 4;
-  static_assert(NA >= 1 && (NBW >= 4 ? NBW % 4 == 0 : true), "tile / stage mismatch");
+  static_assert(NA >= 1 && (NBC >= 4 ? NBC % 4 == 0 : true), "tile / stage mismatch");
+  static_assert(BCH == 1 || RBC == 128, "B chunks are whole 128-byte lines");
   using AccT = typename std::conditional<AK == AK_I8, v16i, v16f>::type;
 
   __shared__ __attribute__((aligned(16))) uint8_t a_s0[kTM * RA];
   __shared__ __attribute__((aligned(16))) uint8_t a_s1[kTM * RA];
-  __shared__ __attribute__((aligned(16))) uint8_t b_s0[TBR * RB];
-  __shared__ __attribute__((aligned(16))) uint8_t b_s1[TBR * RB];
+  __shared__ __attribute__((aligned(16))) uint8_t b_s0[TBR * RBC];
+  __shared__ __attribute__((aligned(16))) uint8_t b_s1[TBR * RBC];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
   const size_t b_row = (size_t)b_row_bytes<BK>(K);
 
   // ---- DMA sources (per lane, per instruction)
-  constexpr int CA = RA / 16, CB = RB / 16;  // chunks per row
+  constexpr int CA = RA / 16, CB = RBC / 16;  // 16-byte chunks per LDS row
   const uint8_t* a_src[NA];
 #pragma unroll
   for (int q = 0; q < NA; q++) {
@@ -234,11 +240,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
     a_src[q] = reinterpret_cast<const uint8_t*>(g.a) + (size_t)min(m0 + r, M - 1) * a_row + c * 16;
   }
   const uint8_t* b_src[NB];
-  const bool b_issuer = NBW >= 4 || wave < NBW;
+  const bool b_issuer = NBC >= 4 || wave < NBC;
 #pragma unroll
   for (int q = 0; q < NB; q++) {
-    const int r = (NBW >= 4 ? wave * NB + q : min(wave, NBW - 1)) * (1024 / RB) + lane / CB;
-    const int c = (lane % CB) ^ swz<RB>(r);
+    const int r = (NBC >= 4 ? wave * NB + q : min(wave, NBC - 1)) * (1024 / RBC) + lane / CB;
+    const int c = (lane % CB) ^ swz<RBC>(r);
     const uint8_t* base;
     int wrow;
     if (DUAL) {
@@ -280,17 +286,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
 
   uint32_t scv[2][NWB];  // 4-bit scales of the stage in flight / in use
 
-#define MXQ_ISSUE(S, AS, BS, P)                                                                    \
+  // A of stage S into slot AS; the 4-bit scales of stage S into register set P.
+#define MXQ_DMA_A(S, AS)                                                                           \
   {                                                                                                \
-    const size_t ka_ = (size_t)(kt0 + (S)) * RA, kb_ = (size_t)(kt0 + (S)) * RB;                   \
+    const size_t ka_ = (size_t)(kt0 + (S)) * RA;                                                   \
     _Pragma("unroll") for (int q = 0; q < NA; q++)                                                 \
       dma16(a_src[q] + ka_, (AS) + (wave * NA + q) * 1024);                                         \
-    if (b_issuer) {                                                                                \
-      _Pragma("unroll") for (int q = 0; q < NB; q++) {                                             \
-        const int qi_ = NBW >= 4 ? wave * NB + q : wave;                                           \
-        dma16(b_src[q] + kb_, (BS) + qi_ * 1024);                                                  \
-      }                                                                                            \
-    }                                                                                              \
+  }
+#define MXQ_SCALES(S, P)                                                                           \
+  {                                                                                                \
     if (SCALES4) {                                                                                 \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
         const uint8_t* p_ = sc_src[j] + (size_t)(S) * (KS / 32) * (BK == BK_INT4G32 ? 2 : 1);     \
@@ -298,16 +302,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
       }                                                                                            \
     }                                                                                              \
   }
-  // vmcnt that leaves exactly one stage (the one just issued) in flight
-  const int vm_stage = NA + (b_issuer ? NB : 0) + (SCALES4 ? NWB : 0);
-
-#define MXQ_WAIT_PREV()                                                                            \
+  // B chunk C (stages C*BCH .. C*BCH + BCH - 1) into slot BS.
+#define MXQ_DMA_B(C, BS)                                                                         \
   {                                                                                                \
-    if (vm_stage == NA + NB + (SCALES4 ? NWB : 0)) __builtin_amdgcn_s_waitcnt(wait_vm(NA + NB + (SCALES4 ? NWB : 0))); \
-    else __builtin_amdgcn_s_waitcnt(wait_vm(NA + (SCALES4 ? NWB : 0)));                             \
+    const size_t kb_ = (size_t)(kt0 + (C) * BCH) * RB;                                             \
+    if (b_issuer) {                                                                                \
+      _Pragma("unroll") for (int q = 0; q < NB; q++) {                                             \
+        const int qi_ = NBC >= 4 ? wave * NB + q : wave;                                           \
+        dma16(b_src[q] + kb_, (BS) + qi_ * 1024);                                                  \
+      }                                                                                            \
+    }                                                                                              \
   }
+  // loads one wave issues per stage (A + scales); a B chunk adds NB
+  constexpr int VM_A = NA + (SCALES4 ? NWB : 0);
 
-#define MXQ_COMPUTE(AS, BS, P)                                                                     \
+#define MXQ_COMPUTE(AS, BS, P, POS)                                                                   \
   {                                                                                                \
     _Pragma("unroll") for (int s = 0; s < KSTEPS; s++) {                                           \
       if (AK == AK_I8) {                                                                           \
@@ -318,7 +327,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
         }                                                                                          \
         _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                           \
           const int r_ = b_blk[j] + r32;                                                           \
-          bf[j] = *reinterpret_cast<const v4i*>((BS) + r_ * RB + (((4 * h + s) ^ swz<RB>(r_)) << 4)); \
+          bf[j] = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + 4 * h + s) ^ swz<RBC>(r_)) << 4)); \
         }                                                                                          \
         _Pragma("unroll") for (int i = 0; i < 2; i++)                                              \
           _Pragma("unroll") for (int j = 0; j < NWB; j++)                                           \
@@ -341,13 +350,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
         _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                           \
           const int r_ = b_blk[j] + r32;                                                           \
           if (BK == BK_F16) {                                                                      \
-            bf[j] = *reinterpret_cast<const v8h*>((BS) + r_ * RB + (((4 * h + s) ^ swz<RB>(r_)) << 4)); \
+            bf[j] = *reinterpret_cast<const v8h*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + 4 * h + s) ^ swz<RBC>(r_)) << 4)); \
           } else if (BK == BK_MXFP4 || BK == BK_INT4G32) {                                         \
-            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RB + ((h ^ swz<RB>(r_)) << 4)); \
+            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + h) ^ swz<RBC>(r_)) << 4)); \
             if (BK == BK_MXFP4) bf[j] = fp4x8_dequant_f16(w_[s], scv[P][j]);                       \
             else bf[j] = i4x8_to_f16(w_[s], __builtin_bit_cast(_Float16, (uint16_t)scv[P][j]));    \
           } else {                                                                                 \
-            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RB + (((2 * h + (s >> 1)) ^ swz<RB>(r_)) << 4)); \
+            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + 2 * h + (s >> 1)) ^ swz<RBC>(r_)) << 4)); \
             const uint32_t w0_ = (s & 1) ? w_[2] : w_[0], w1_ = (s & 1) ? w_[3] : w_[1];          \
             if (BK == BK_INT8) bf[j] = i8x8_to_f16(w0_, w1_);                                      \
             else bf[j] = fp8x8_to_f16<BK>(w0_, w1_);                                               \
@@ -360,36 +369,72 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
     }                                                                                              \
   }
 
-  // Pipeline: stage k+1's DMA is in flight while stage k is computed.
-  // Scheduling barriers keep each stage's DMA issue, wait and barrier in
-  // place: otherwise the compiler hoists the next stage's scale arithmetic
-  // above the partial wait and has to drain every load first.
+  // Pipeline, one B stage per A stage (BCH = 1): stage k+1's DMA is in
+  // flight while stage k is computed.  Scheduling barriers keep each stage's
+  // DMA issue, wait and barrier in place: otherwise the compiler hoists the
+  // next stage's scale arithmetic above the partial wait and has to drain
+  // every load first.
+#define MXQ_ISSUE(S, AS, BS, P) MXQ_DMA_A(S, AS) MXQ_DMA_B(S, BS) MXQ_SCALES(S, P)
 #define MXQ_SYNC_POINT()                                                                           \
   __builtin_amdgcn_sched_barrier(0);                                                               \
-  MXQ_WAIT_PREV()                                                                                  \
+  if (b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm(VM_A + NB));                                    \
+  else __builtin_amdgcn_s_waitcnt(wait_vm(VM_A));                                                  \
   __builtin_amdgcn_s_barrier();                                                                    \
   __builtin_amdgcn_sched_barrier(0);
+  // Chunked B (BCH > 1): stage st issues stage st+1's A (and, on a chunk's
+  // first stage, the next chunk's B) and scales, waits until only those are
+  // in flight, computes st behind a barrier and frees its slots with a
+  // second barrier.  vmcnt retires in issue order, so the wait also covers
+  // the B chunk issued one chunk earlier.  The body is unrolled over 2 * BCH
+  // stages so that every LDS slot is a constant.
+#define MXQ_BODY(U)                                                                                \
+  if constexpr ((U) < 2 * BCH) {                                                                   \
+    if (kt + (U) < KT) {                                                                           \
+      constexpr int AP_ = (U) & 1, BP_ = ((U) / BCH) & 1, POS_ = (U) % BCH;                        \
+      const int st_ = kt + (U);                                                                    \
+      MXQ_DMA_A(min(st_ + 1, KT - 1), (AP_ ? a_s0 : a_s1))                                         \
+      if (POS_ == 0) MXQ_DMA_B(min(st_ / BCH + 1, KT / BCH - 1), (BP_ ? b_s0 : b_s1))              \
+      MXQ_SCALES(min(st_ + 1, KT - 1), AP_ ^ 1)                                                    \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+      if (POS_ == 0 && b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm(VM_A + NB));                   \
+      else __builtin_amdgcn_s_waitcnt(wait_vm(VM_A));                                              \
+      __builtin_amdgcn_s_barrier();                                                                \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+      MXQ_COMPUTE((AP_ ? a_s1 : a_s0), (BP_ ? b_s1 : b_s0), AP_, POS_)                             \
+      __builtin_amdgcn_s_barrier();                                                                \
+    }                                                                                              \
+  }
   MXQ_ISSUE(0, a_s0, b_s0, 0)
-  int kt = 0;
-  for (; kt + 2 <= KT; kt += 2) {
-    MXQ_ISSUE(kt + 1, a_s1, b_s1, 1)
-    MXQ_SYNC_POINT()
-    MXQ_COMPUTE(a_s0, b_s0, 0)
-    __builtin_amdgcn_s_barrier();  // slot 0 free
-    MXQ_ISSUE(min(kt + 2, KT - 1), a_s0, b_s0, 0)
-    MXQ_SYNC_POINT()
-    MXQ_COMPUTE(a_s1, b_s1, 1)
-    __builtin_amdgcn_s_barrier();  // slot 1 free
+  if constexpr (BCH == 1) {
+    int kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+      MXQ_ISSUE(kt + 1, a_s1, b_s1, 1)
+      MXQ_SYNC_POINT()
+      MXQ_COMPUTE(a_s0, b_s0, 0, 0)
+      __builtin_amdgcn_s_barrier();  // slot 0 free
+      MXQ_ISSUE(min(kt + 2, KT - 1), a_s0, b_s0, 0)
+      MXQ_SYNC_POINT()
+      MXQ_COMPUTE(a_s1, b_s1, 1, 0)
+      __builtin_amdgcn_s_barrier();  // slot 1 free
+    }
+    if (kt < KT) {  // odd stage count: the last stage sits in slot 0
+      __builtin_amdgcn_s_waitcnt(wait_vm(0));
+      __builtin_amdgcn_s_barrier();
+      MXQ_COMPUTE(a_s0, b_s0, 0, 0)
+    }
+  } else {
+    for (int kt = 0; kt < KT; kt += 2 * BCH) {
+      MXQ_BODY(0) MXQ_BODY(1) MXQ_BODY(2) MXQ_BODY(3)
+      MXQ_BODY(4) MXQ_BODY(5) MXQ_BODY(6) MXQ_BODY(7)
+    }
   }
+#undef MXQ_BODY
 #undef MXQ_SYNC_POINT
-  if (kt < KT) {  // odd stage count: the last stage sits in slot 0
-    __builtin_amdgcn_s_waitcnt(wait_vm(0));
-    __builtin_amdgcn_s_barrier();
-    MXQ_COMPUTE(a_s0, b_s0, 0)
-  }
-  __builtin_amdgcn_s_waitcnt(0);
 #undef MXQ_ISSUE
-#undef MXQ_WAIT_PREV
+  __builtin_amdgcn_s_waitcnt(0);
+#undef MXQ_DMA_A
+#undef MXQ_DMA_B
+#undef MXQ_SCALES
 #undef MXQ_COMPUTE
 
   // ---- epilogue, or the raw partial tile when K is split (separate loops
@@ -486,14 +531,27 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
   epi_store<EPI>(g.c, o, x0, u);
 }
 
+// Stages per B chunk that make a chunk one 128-byte line per weight row.
+// (4-bit weights only: for 8-bit rows the chunked loop measured no faster)
+template <int AK, int BK> constexpr int b_chunk() {
+  return (BK == BK_MXFP4 || BK == BK_INT4G32) ? 128 / b_row_bytes<BK>(AInfo<AK>::KS) : 1;
+}
+
 template <int AK, int BK, int EPI, int NWB>
 hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   QGemmArgs g = g0;
   g.tiles_m = (g.m + kTM - 1) / kTM;
   const int tiles_n = is_dual(EPI) ? g.n / 64 : g.n / (NWB * 64);
+  constexpr int BC = b_chunk<AK, BK>();
+  const int kt = g.k / AInfo<AK>::KS / splits;  // stages per split
   // (the ungrouped form's second argument is an unused int: a sized type
   // keeps the host and device kernel-argument layouts identical)
-  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
+  // chunked B once a split spans at least four chunks (a shorter split would
+  // wait for its whole B up front)
+  if (BC > 1 && kt % BC == 0 && kt >= 4 * BC)
+    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
+  else
+    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
   if (splits > 1) {
     const size_t n = (size_t)g.m * g.n;
     hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, splits);
@@ -515,8 +573,13 @@ hipError_t launch_q_grouped(const QGemmArgs& g0, const GroupTable& gt, int group
   QGemmArgs g = g0;
   g.tiles_m = (g.m + kTM - 1) / kTM;
   const int tiles_n = is_dual(EPI) ? g.n / 64 : g.n / (NWB * 64);
-  hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true>), dim3(g.tiles_m * tiles_n, 1, groups), dim3(256), 0, st, g,
-                     gt);
+  constexpr int BC = b_chunk<AK, BK>();
+  if (BC > 1 && (g.k / AInfo<AK>::KS) % BC == 0 && g.k / AInfo<AK>::KS >= 4 * BC)
+    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, BC>), dim3(g.tiles_m * tiles_n, 1, groups), dim3(256), 0, st,
+                       g, gt);
+  else
+    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, 1>), dim3(g.tiles_m * tiles_n, 1, groups), dim3(256), 0, st,
+                       g, gt);
   return hipGetLastError();
 }
 
