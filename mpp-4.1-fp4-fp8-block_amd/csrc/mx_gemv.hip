@@ -40,7 +40,9 @@ namespace mx {
 constexpr int kStepK = 128;   // K per lane step: 4 lane groups x 32-element blocks
 // NSTEP: steps per wave whose weight loads are issued together (2, 4 or 8).
 constexpr int kW = 8;         // waves per workgroup
-constexpr int kMaxScaleRegs = 4;  // scale dwords staged per thread: K <= 16384 / row groups
+// scale dwords staged per thread: 4 up to two row groups per workgroup
+// (K <= 16384), 8 for four (launchers check K)
+constexpr int scale_regs(int ng) { return ng <= 2 ? 4 : 8; }
 
 // 16-byte global -> LDS DMA of one lane (LDS base wave-uniform).
 __device__ __forceinline__ void dma16(const void* src, void* lds) {
@@ -66,7 +68,7 @@ __host__ __device__ inline size_t gemv_lds_bytes(int t, int k, int ng = 1) {
 template <bool DUAL, int NSTEP, int WPG>
 __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* lds) {
   constexpr int NG = kW / WPG;
-  static_assert(NG * WPG == kW && NG <= 2, "row groups per workgroup");
+  static_assert(NG * WPG == kW && NG <= 4, "row groups per workgroup");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int gi = wave / WPG, gw = wave % WPG;  // this wave's group and its index in the group
   const int r = lane & 15, lg = lane >> 4;
@@ -110,9 +112,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
     }
   }
   const int n_sdw = 16 * NG * (KB / 4);  // scale dwords of the workgroup's rows
-  uint32_t sreg[kMaxScaleRegs];
+  constexpr int SREGS = scale_regs(NG);
+  uint32_t sreg[SREGS];
 #pragma unroll
-  for (int q = 0; q < kMaxScaleRegs; q++) {
+  for (int q = 0; q < SREGS; q++) {
     const int i = min(tid + q * 64 * kW, n_sdw - 1);  // clamped: no predicated loads
     const int wr = i / (KB / 4), c = i % (KB / 4);
     const uint8_t* w;
@@ -137,7 +140,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   //    the weights).
   __builtin_amdgcn_s_waitcnt(gemv_wait_vm(NSTEP));
 #pragma unroll
-  for (int q = 0; q < kMaxScaleRegs; q++) {
+  for (int q = 0; q < SREGS; q++) {
     const int i = tid + q * 64 * kW;
     if (i < n_sdw) {
       const int wr = i / (KB / 4), c = i % (KB / 4);
@@ -231,8 +234,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
 #pragma unroll
   for (int v = 0; v < 4; v++) red[(wave * 16 + lg * 4 + v) * 17 + r] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
   __syncthreads();
-  if (tid < NG * 256) {  // whole waves: thread (group g2, token tt, column cc)
-    const int g2 = tid >> 8, tt = (tid >> 4) & 15, cc = tid & 15;
+  // whole waves: thread (group g2, token tt, column cc), two groups per pass
+#pragma unroll
+  for (int g2 = tid >> 8; g2 < NG; g2 += 2) {
+    const int tt = (tid >> 4) & 15, cc = tid & 15;
     const int grp = g0 + g2;
     float tot = 0.0f;
 #pragma unroll
@@ -340,16 +345,22 @@ static hipError_t launch_grouped_w(const GemvArgs& g, const GroupTable& gt, int 
 }
 
 // g.t = the largest group's token count (sizes the LDS); the same
-// preconditions as launch_gemv_mxfp4 for it.  With many workgroups
-// (groups x row groups >= 1024) each workgroup takes two row groups, four
-// waves each, so x is staged once for 32 weight rows.
+// preconditions as launch_gemv_mxfp4 for it.  With many workgroups each one
+// takes several row groups, so x (T x K, staged per workgroup) is staged
+// once for more weight rows: two row groups (four waves each) from 1024
+// one-group workgroups on, four (two waves each) from 4096 on (measured at
+// 64 experts x 4 tokens of the C1 shape: gate/up 254 -> 241 us, down
+// 128 -> 116 us against two).
 hipError_t launch_gemv_mxfp4_grouped(int dual, const GemvArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
   const int row_groups = dual ? g.n / 8 : g.n / 16;
-  const bool pair = (size_t)groups * row_groups >= 1024 && row_groups % 2 == 0 && g.k <= 8192 &&
-                    gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
+  const size_t wg1 = (size_t)groups * row_groups;  // workgroups at one row group each
+  const bool pair = wg1 >= 1024 && row_groups % 2 == 0 && g.k <= 8192 && gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
+  const bool quad = wg1 >= 4096 && row_groups % 4 == 0 && 16 * 4 * (g.k / 128) <= scale_regs(4) * 64 * kW &&
+                    gemv_lds_bytes(g.t, g.k, 4) <= 160 * 1024;
   if (groups < 1 || groups > kMaxGroups || g.t < 1 || g.t > 16 || gemv_lds_bytes(g.t, g.k) > 160 * 1024 ||
       g.k > 16384 || g.k % kStepK)
     return hipErrorInvalidValue;
+  if (quad) return dual ? launch_grouped_w<true, kW / 4>(g, gt, groups, st) : launch_grouped_w<false, kW / 4>(g, gt, groups, st);
   if (pair) return dual ? launch_grouped_w<true, kW / 2>(g, gt, groups, st) : launch_grouped_w<false, kW / 2>(g, gt, groups, st);
   return dual ? launch_grouped_w<true, kW>(g, gt, groups, st) : launch_grouped_w<false, kW>(g, gt, groups, st);
 }

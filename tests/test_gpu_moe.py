@@ -75,7 +75,9 @@ def check(got, ref, what):
     ([4] * 12, 256, 512),                   # many experts
     ([0, 0, 1], 128, 256),                  # only the last expert has work
     ([3, 0, 5, 1, 2, 4, 0, 1, 5, 3, 2, 1, 4, 0, 2, 3, 1, 5, 2, 1], 1024, 1024),  # >= 1024 workgroups:
-])                                                                            # two row groups each
+                                                                              # two row groups each
+    ([i % 5 for i in range(64)], 1024, 512),  # >= 4096 one-group workgroups in both launches: four each
+])
 def test_moe_decode_experts(dev, counts, H, I):
     d = MoeData(dev, counts, H, I, seed=len(counts) + H)
     got = d.run()
