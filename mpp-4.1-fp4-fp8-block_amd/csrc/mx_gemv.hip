@@ -41,8 +41,8 @@ constexpr int kStepK = 128;   // K per lane step: 4 lane groups x 32-element blo
 // NSTEP: steps per wave whose weight loads are issued together (2, 4 or 8).
 constexpr int kW = 8;         // waves per workgroup
 // scale dwords staged per thread: 4 up to two row groups per workgroup
-// (K <= 16384), 8 for four (launchers check K)
-constexpr int scale_regs(int ng) { return ng <= 2 ? 4 : 8; }
+// (K <= 16384), 8 for four and 16 for eight (launchers check K)
+constexpr int scale_regs(int ng) { return ng <= 2 ? 4 : ng <= 4 ? 8 : 16; }
 
 // 16-byte global -> LDS DMA of one lane (LDS base wave-uniform).
 __device__ __forceinline__ void dma16(const void* src, void* lds) {
@@ -68,7 +68,7 @@ __host__ __device__ inline size_t gemv_lds_bytes(int t, int k, int ng = 1) {
 template <bool DUAL, int NSTEP, int WPG>
 __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* lds) {
   constexpr int NG = kW / WPG;
-  static_assert(NG * WPG == kW && NG <= 4, "row groups per workgroup");
+  static_assert(NG * WPG == kW && NG <= 8, "row groups per workgroup");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int gi = wave / WPG, gw = wave % WPG;  // this wave's group and its index in the group
   const int r = lane & 15, lg = lane >> 4;
@@ -348,18 +348,22 @@ static hipError_t launch_grouped_w(const GemvArgs& g, const GroupTable& gt, int 
 // preconditions as launch_gemv_mxfp4 for it.  With many workgroups each one
 // takes several row groups, so x (T x K, staged per workgroup) is staged
 // once for more weight rows: two row groups (four waves each) from 1024
-// one-group workgroups on, four (two waves each) from 4096 on (measured at
-// 64 experts x 4 tokens of the C1 shape: gate/up 254 -> 241 us, down
-// 128 -> 116 us against two).
+// one-group workgroups on, four (two waves each) from 4096 on, eight (one
+// wave each) from 8192 on while two workgroups still fit a CU (measured at
+// 64 experts x 4 tokens of the C1 shape: gate/up 254 -> 241 us with four,
+// down 128 -> 115 us with four and 109 us with eight).
 hipError_t launch_gemv_mxfp4_grouped(int dual, const GemvArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
   const int row_groups = dual ? g.n / 8 : g.n / 16;
   const size_t wg1 = (size_t)groups * row_groups;  // workgroups at one row group each
   const bool pair = wg1 >= 1024 && row_groups % 2 == 0 && g.k <= 8192 && gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
   const bool quad = wg1 >= 4096 && row_groups % 4 == 0 && 16 * 4 * (g.k / 128) <= scale_regs(4) * 64 * kW &&
                     gemv_lds_bytes(g.t, g.k, 4) <= 160 * 1024;
+  const bool octo = wg1 >= 8192 && row_groups % 8 == 0 && 16 * 8 * (g.k / 128) <= scale_regs(8) * 64 * kW &&
+                    gemv_lds_bytes(g.t, g.k, 8) <= 80 * 1024;  // still two workgroups per CU
   if (groups < 1 || groups > kMaxGroups || g.t < 1 || g.t > 16 || gemv_lds_bytes(g.t, g.k) > 160 * 1024 ||
       g.k > 16384 || g.k % kStepK)
     return hipErrorInvalidValue;
+  if (octo) return dual ? launch_grouped_w<true, kW / 8>(g, gt, groups, st) : launch_grouped_w<false, kW / 8>(g, gt, groups, st);
   if (quad) return dual ? launch_grouped_w<true, kW / 4>(g, gt, groups, st) : launch_grouped_w<false, kW / 4>(g, gt, groups, st);
   if (pair) return dual ? launch_grouped_w<true, kW / 2>(g, gt, groups, st) : launch_grouped_w<false, kW / 2>(g, gt, groups, st);
   return dual ? launch_grouped_w<true, kW>(g, gt, groups, st) : launch_grouped_w<false, kW>(g, gt, groups, st);

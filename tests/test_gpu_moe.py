@@ -77,6 +77,7 @@ def check(got, ref, what):
     ([3, 0, 5, 1, 2, 4, 0, 1, 5, 3, 2, 1, 4, 0, 2, 3, 1, 5, 2, 1], 1024, 1024),  # >= 1024 workgroups:
                                                                               # two row groups each
     ([i % 5 for i in range(64)], 1024, 512),  # >= 4096 one-group workgroups in both launches: four each
+    ([i % 4 for i in range(128)], 1024, 256),  # down >= 8192: eight each; gate/up four
 ])
 def test_moe_decode_experts(dev, counts, H, I):
     d = MoeData(dev, counts, H, I, seed=len(counts) + H)
