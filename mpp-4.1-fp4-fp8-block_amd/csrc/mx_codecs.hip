@@ -239,34 +239,55 @@ __global__ void k_swiglu(int variant, const void* __restrict__ gate, const void*
 // fmt 1 = FP8 E4M3 / 2 = FP8 E5M2 (scale amax/qmax), 3 = INT8 (amax/127).
 // Division in f32, matching the CPU oracle bit for bit.
 // Also the per-token INT8 activation quantizer of W8A8 (SRC_F16: x in f16).
+
+// 4 consecutive elements of row data (k % 4 == 0, so chunk c stays in the row
+// and is 8- or 16-byte aligned).
 template <bool SRC_F16>
-__device__ __forceinline__ float ld_src(const void* p, size_t i) {
-  if (SRC_F16) return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-  return reinterpret_cast<const float*>(p)[i];
+__device__ __forceinline__ void ld_src4(const void* p, size_t base, int c, float v[4]) {
+  if (SRC_F16) {
+    const uint2 u = reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + base)[c];
+    v[0] = f16_bits_to_f32((uint16_t)(u.x & 0xffffu));
+    v[1] = f16_bits_to_f32((uint16_t)(u.x >> 16));
+    v[2] = f16_bits_to_f32((uint16_t)(u.y & 0xffffu));
+    v[3] = f16_bits_to_f32((uint16_t)(u.y >> 16));
+  } else {
+    const float4 f = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + base)[c];
+    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+  }
 }
 
+// One workgroup (512 threads) per row: amax (wave shuffles, one barrier),
+// scale = amax / qmax, then every element v / scale to the format.  The row
+// is read twice (the second pass from cache), 4 elements per load.
 template <bool SRC_F16>
-__global__ void k_quant_rowwise(int fmt, const void* __restrict__ w, int k,
-                                uint8_t* __restrict__ q, float* __restrict__ row_scale) {
-  __shared__ float red[256];
-  const int row = blockIdx.x;
+__global__ __launch_bounds__(512) void k_quant_rowwise(int fmt, const void* __restrict__ w, int k,
+                                                       uint8_t* __restrict__ q, float* __restrict__ row_scale) {
+  __shared__ float red[8];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const size_t base = (size_t)row * k;
+  const int nch = k / 4;
   float amax = 0.0f;
-  for (int i = threadIdx.x; i < k; i += blockDim.x) amax = fmaxf(amax, fabsf(ld_src<SRC_F16>(w, base + i)));
-  red[threadIdx.x] = amax;
-  __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-    __syncthreads();
+  for (int c = tid; c < nch; c += 512) {
+    float v[4];
+    ld_src4<SRC_F16>(w, base, c, v);
+#pragma unroll
+    for (int t = 0; t < 4; t++) amax = fmaxf(amax, fabsf(v[t]));
   }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if (lane == 0) red[tid >> 6] = amax;
+  __syncthreads();
   amax = red[0];
+#pragma unroll
+  for (int i = 1; i < 8; i++) amax = fmaxf(amax, red[i]);
   const float qmax = fmt == 1 ? 448.0f : fmt == 2 ? 57344.0f : 127.0f;
   const float sc = amax > 0.0f ? amax / qmax : 1.0f;
-  if (threadIdx.x == 0) row_scale[row] = sc;
-  uint8_t* dst = q + (size_t)row * k;
-  for (int i = threadIdx.x * 4; i < k; i += blockDim.x * 4) {
-    const float v0 = ld_src<SRC_F16>(w, base + i) / sc, v1 = ld_src<SRC_F16>(w, base + i + 1) / sc,
-                v2 = ld_src<SRC_F16>(w, base + i + 2) / sc, v3 = ld_src<SRC_F16>(w, base + i + 3) / sc;
+  if (tid == 0) row_scale[row] = sc;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(q + base);
+  for (int c = tid; c < nch; c += 512) {
+    float v[4];
+    ld_src4<SRC_F16>(w, base, c, v);
+    const float v0 = v[0] / sc, v1 = v[1] / sc, v2 = v[2] / sc, v3 = v[3] / sc;
     uint32_t r;
     if (fmt == 1) r = fp8x4_from_f32<false>(v0, v1, v2, v3);
     else if (fmt == 2) r = fp8x4_from_f32<true>(v0, v1, v2, v3);
@@ -279,7 +300,7 @@ __global__ void k_quant_rowwise(int fmt, const void* __restrict__ w, int k,
         r |= ((uint32_t)(int)rv & 0xffu) << (8 * t);
       }
     }
-    *reinterpret_cast<uint32_t*>(dst + i) = r;
+    dst[c] = r;
   }
 }
 
@@ -405,7 +426,8 @@ hipError_t launch_swiglu(int variant, const void* gate, const void* up, void* mi
 hipError_t launch_quant_rowwise(int fmt, const float* w, int rows, int k, uint8_t* q, float* scale,
                                 hipStream_t st) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quant_rowwise<false>, dim3(rows), dim3(256), 0, st, fmt, w, k, q, scale);
+  if (k % 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_quant_rowwise<false>, dim3(rows), dim3(512), 0, st, fmt, w, k, q, scale);
   return hipGetLastError();
 }
 
@@ -414,11 +436,12 @@ hipError_t launch_quant_rowwise(int fmt, const float* w, int rows, int k, uint8_
 hipError_t launch_quant_act_int8(const void* x, int x_dtype, int rows, int k, int8_t* q,
                                  float* scale, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
+  if (k % 4) return hipErrorInvalidValue;
   if (x_dtype == MX_DTYPE_F16)
-    hipLaunchKernelGGL(k_quant_rowwise<true>, dim3(rows), dim3(256), 0, st, 3, x, k,
+    hipLaunchKernelGGL(k_quant_rowwise<true>, dim3(rows), dim3(512), 0, st, 3, x, k,
                        reinterpret_cast<uint8_t*>(q), scale);
   else
-    hipLaunchKernelGGL(k_quant_rowwise<false>, dim3(rows), dim3(256), 0, st, 3, x, k,
+    hipLaunchKernelGGL(k_quant_rowwise<false>, dim3(rows), dim3(512), 0, st, 3, x, k,
                        reinterpret_cast<uint8_t*>(q), scale);
   return hipGetLastError();
 }
