@@ -497,38 +497,57 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
   }
 }
 
-// Split-K reduction + epilogue: one thread per output element.
+// Split-K reduction + epilogue: four consecutive output elements per thread
+// (m * n % 4 == 0 since n % 64 == 0), 16-byte loads from the 256-byte
+// aligned partial planes; each element still sums its splits in split order.
 template <int AK, int BK, int EPI>
 __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
   constexpr bool DUAL = is_dual(EPI);
   constexpr int PL = DUAL ? 2 : 1;
   const size_t plane = (size_t)g.m * g.n;
-  const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (o >= plane) return;
   const int row = (int)(o / g.n), col = (int)(o % g.n);
   const uint32_t* w = reinterpret_cast<const uint32_t*>(g.ws);
-  float sums[2];
+  auto ld4 = [&](size_t idx) { return *reinterpret_cast<const uint4*>(w + idx); };
   if (EPI == EPI_STORE_I32) {
-    int s = 0;
-    for (int k = 0; k < splits; k++) s += (int)w[(size_t)k * plane + o];
-    reinterpret_cast<int*>(g.c)[o] = s;
+    int s[4] = {0, 0, 0, 0};
+    for (int k = 0; k < splits; k++) {
+      const uint4 v = ld4((size_t)k * plane + o);
+      s[0] += (int)v.x; s[1] += (int)v.y; s[2] += (int)v.z; s[3] += (int)v.w;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) reinterpret_cast<int*>(g.c)[o + t] = s[t];  // caller's buffer: 4-byte aligned
     return;
   }
+  float sums[2][4];
 #pragma unroll
   for (int p = 0; p < PL; p++) {
     if (AK == AK_I8) {
-      int s = 0;
-      for (int k = 0; k < splits; k++) s += (int)w[((size_t)k * PL + p) * plane + o];
-      sums[p] = (float)s;
+      int s[4] = {0, 0, 0, 0};
+      for (int k = 0; k < splits; k++) {
+        const uint4 v = ld4(((size_t)k * PL + p) * plane + o);
+        s[0] += (int)v.x; s[1] += (int)v.y; s[2] += (int)v.z; s[3] += (int)v.w;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) sums[p][t] = (float)s[t];
     } else {
-      float s = 0.0f;
-      for (int k = 0; k < splits; k++) s += __builtin_bit_cast(float, w[((size_t)k * PL + p) * plane + o]);
-      sums[p] = s;
+      float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int k = 0; k < splits; k++) {
+        const uint4 v = ld4(((size_t)k * PL + p) * plane + o);
+        s[0] += __builtin_bit_cast(float, v.x); s[1] += __builtin_bit_cast(float, v.y);
+        s[2] += __builtin_bit_cast(float, v.z); s[3] += __builtin_bit_cast(float, v.w);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) sums[p][t] = s[t];
     }
   }
-  const float x0 = scaled<AK, BK>(sums[0], g, reinterpret_cast<const float*>(g.s0), row, col);
-  const float u = DUAL ? scaled<AK, BK>(sums[PL - 1], g, reinterpret_cast<const float*>(g.s1), row, col) : 0.0f;
-  epi_store<EPI>(g.c, o, x0, u);
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const float x0 = scaled<AK, BK>(sums[0][t], g, reinterpret_cast<const float*>(g.s0), row, col + t);
+    const float u = DUAL ? scaled<AK, BK>(sums[PL - 1][t], g, reinterpret_cast<const float*>(g.s1), row, col + t) : 0.0f;
+    epi_store<EPI>(g.c, o + t, x0, u);
+  }
 }
 
 // Stages per B chunk that make a chunk one 128-byte line per weight row.
@@ -554,7 +573,7 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
     hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
   if (splits > 1) {
     const size_t n = (size_t)g.m * g.n;
-    hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, splits);
+    hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st, g, splits);
   }
   return hipGetLastError();
 }
