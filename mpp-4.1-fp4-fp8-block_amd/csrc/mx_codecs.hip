@@ -181,21 +181,19 @@ __global__ void k_mxfp4_quantize(const void* __restrict__ src, uint8_t* __restri
 }
 
 // ---------------------------------------------------------------------------
-// Dequant to half (MXFP4Kernels.metal:509-538): one thread per 32-element
-// block, 16 packed bytes in, 64 bytes out, one v_cvt_scalef32_pk_f16_fp4 per
-// two values.  E8M0 byte 255 decodes to +inf in the reference (bits<<23);
-// the hardware would read it as NaN, so that block takes the exact path.
+// Dequant to half (MXFP4Kernels.metal:509-538): one thread per 8 elements
+// (one dword of codes in, one 16-byte store out, so a wave writes 1 KB of
+// contiguous output), one v_cvt_scalef32_pk_f16_fp4 per two values.  E8M0
+// byte 255 decodes to +inf in the reference (bits<<23); the hardware would
+// read it as NaN, so those codes take the exact path.
 __global__ void k_mxfp4_dequant_f16(const uint8_t* __restrict__ packed,
                                     const uint8_t* __restrict__ scales,
-                                    uint16_t* __restrict__ out, size_t nblocks) {
-  size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= nblocks) return;
-  uint4 w = reinterpret_cast<const uint4*>(packed)[b];
-  uint32_t sb = scales[b];
-  uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-  uint4* o = reinterpret_cast<uint4*>(out + b * 32);
-#pragma unroll
-  for (int q = 0; q < 4; q++) o[q] = __builtin_bit_cast(uint4, fp4x8_dequant_f16(ws[q], sb));
+                                    uint16_t* __restrict__ out, size_t nwords) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // dword of codes
+  if (i >= nwords) return;
+  const uint32_t w = reinterpret_cast<const uint32_t*>(packed)[i];
+  const uint32_t sb = scales[i / 4];  // 4 dwords per 32-element block
+  reinterpret_cast<uint4*>(out)[i] = __builtin_bit_cast(uint4, fp4x8_dequant_f16(w, sb));
 }
 
 // ---------------------------------------------------------------------------
@@ -408,10 +406,10 @@ hipError_t launch_mxfp4_quantize(const void* src, int src_dtype, uint8_t* packed
 
 hipError_t launch_mxfp4_dequant_f16(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
                                     size_t rows, size_t depth, hipStream_t st) {
-  size_t nblocks = rows * (depth / 32);
-  if (nblocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_mxfp4_dequant_f16, dim3(grid_for(nblocks, 256)), dim3(256), 0, st, packed,
-                     scales, out, nblocks);
+  const size_t nwords = rows * (depth / 32) * 4;
+  if (nwords == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_mxfp4_dequant_f16, dim3(grid_for(nwords, 256)), dim3(256), 0, st, packed,
+                     scales, out, nwords);
   return hipGetLastError();
 }
 
