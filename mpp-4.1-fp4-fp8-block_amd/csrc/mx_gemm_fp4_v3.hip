@@ -252,8 +252,9 @@ bool w4a4_stage_major_ok(int hidden, int inter) {
 // ---------------------------------------------------------------------------
 // Prologue: blocks [0, qb) quantize x (one thread per 32-element block, E8M0
 // per BASELINE, stage-major scales); the rest convert the three weight scale
-// planes from [rows][K/32] to stage-major (one thread per row and stage).
-__global__ void k_w4a4_prologue(W4A4Prologue p, unsigned qb) {
+// planes from [rows][K/32] to stage-major (one 64 x 32 tile per block for
+// large planes, one dword per thread for small ones).
+__global__ void k_w4a4_prologue(W4A4Prologue p, unsigned qb, int tiled) {
   const size_t Tpad = stage_major_rows(p.t);
   if (blockIdx.x < qb) {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // block index
@@ -287,38 +288,86 @@ __global__ void k_w4a4_prologue(W4A4Prologue p, unsigned qb) {
     p.xs[((blk >> 2) * Tpad + row) * 4 + (blk & 3)] = (uint8_t)sb;
     return;
   }
-  // scale-plane conversion: item = (matrix, stage, row)
-  size_t it = (size_t)(blockIdx.x - qb) * blockDim.x + threadIdx.x;
-  const size_t gate_items = (size_t)p.i * (p.h / 128), down_items = (size_t)p.h * (p.i / 128);
-  const uint8_t* src;
-  uint8_t* dst;
-  size_t rows, stages;
-  if (it < 2 * gate_items) {
-    const bool up = it >= gate_items;
-    if (up) it -= gate_items;
-    src = up ? p.su : p.sg;
-    dst = up ? p.su2 : p.sg2;
-    rows = p.i;
-    stages = p.h / 128;
-  } else {
-    it -= 2 * gate_items;
-    if (it >= down_items) return;
-    src = p.sd;
-    dst = p.sd2;
-    rows = p.h;
-    stages = p.i / 128;
+  if (!tiled) {  // small planes: one thread per (matrix, stage, row) dword
+    size_t it = (size_t)(blockIdx.x - qb) * blockDim.x + threadIdx.x;
+    const size_t gate_items = (size_t)p.i * (p.h / 128), down_items = (size_t)p.h * (p.i / 128);
+    const uint8_t* src;
+    uint8_t* dst;
+    size_t rows, stages;
+    if (it < 2 * gate_items) {
+      const bool up = it >= gate_items;
+      if (up) it -= gate_items;
+      src = up ? p.su : p.sg;
+      dst = up ? p.su2 : p.sg2;
+      rows = p.i;
+      stages = p.h / 128;
+    } else {
+      it -= 2 * gate_items;
+      if (it >= down_items) return;
+      src = p.sd;
+      dst = p.sd2;
+      rows = p.h;
+      stages = p.i / 128;
+    }
+    const size_t row = it % rows, stage = it / rows;  // consecutive threads: consecutive rows
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(src + row * (stages * 4) + stage * 4);
+    *reinterpret_cast<uint32_t*>(dst + (stage * rows + row) * 4) = v;
+    return;
   }
-  const size_t row = it % rows, stage = it / rows;  // consecutive threads: consecutive rows
-  const uint32_t v = *reinterpret_cast<const uint32_t*>(src + row * (stages * 4) + stage * 4);
-  *reinterpret_cast<uint32_t*>(dst + (stage * rows + row) * 4) = v;
+  // scale-plane conversion, one 64-row x 32-stage tile per workgroup:
+  // [rows][stages] dwords (a row's four E8M0 bytes of one 128-K stage) ->
+  // [stages][rows], transposed through LDS so that reads (128 bytes of a
+  // row) and writes (256 bytes of a plane) are both contiguous.
+  __shared__ uint32_t tile[64][33];
+  unsigned t = blockIdx.x - qb;
+  const int gs = p.h / 128, ds = p.i / 128;  // stages of gate/up and of down
+  const unsigned gr = (p.i + 63) / 64, gc = (gs + 31) / 32, dr = (p.h + 63) / 64, dc = (ds + 31) / 32;
+  const uint32_t* src;
+  uint32_t* dst;
+  int rows, stages;
+  unsigned nr;
+  if (t < 2 * gr * gc) {
+    const bool up = t >= gr * gc;
+    if (up) t -= gr * gc;
+    src = reinterpret_cast<const uint32_t*>(up ? p.su : p.sg);
+    dst = reinterpret_cast<uint32_t*>(up ? p.su2 : p.sg2);
+    rows = p.i;
+    stages = gs;
+    nr = gr;
+  } else {
+    t -= 2 * gr * gc;
+    if (t >= dr * dc) return;  // workgroup-uniform
+    src = reinterpret_cast<const uint32_t*>(p.sd);
+    dst = reinterpret_cast<uint32_t*>(p.sd2);
+    rows = p.h;
+    stages = ds;
+    nr = dr;
+  }
+  const int row0 = (int)(t % nr) * 64, s0 = (int)(t / nr) * 32;
+#pragma unroll
+  for (int q = 0; q < 8; q++) {  // consecutive threads: consecutive stages of a row
+    const int idx = q * 256 + (int)threadIdx.x, r = idx / 32, c = idx % 32;
+    if (row0 + r < rows && s0 + c < stages) tile[r][c] = src[(size_t)(row0 + r) * stages + s0 + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; q++) {  // consecutive threads: consecutive rows of a plane
+    const int idx = q * 256 + (int)threadIdx.x, c = idx / 64, r = idx % 64;
+    if (row0 + r < rows && s0 + c < stages) dst[(size_t)(s0 + c) * rows + row0 + r] = tile[r][c];
+  }
 }
 
 hipError_t launch_w4a4_prologue(const W4A4Prologue& p, hipStream_t st) {
   const size_t qitems = (size_t)p.t * (p.h / 32);
-  const size_t sitems = 2 * (size_t)p.i * (p.h / 128) + (size_t)p.h * (p.i / 128);
   const unsigned qb = (unsigned)((qitems + 255) / 256);
-  const unsigned sbk = (unsigned)((sitems + 255) / 256);
-  hipLaunchKernelGGL(k_w4a4_prologue, dim3(qb + sbk), dim3(256), 0, st, p, qb);
+  const unsigned gs = p.h / 128, ds = p.i / 128;
+  const size_t sitems = 2 * (size_t)p.i * gs + (size_t)p.h * ds;
+  // the tiled transpose pays off from ~1M scale dwords (C4: 5.5M); below
+  // that the per-dword copy launches fewer idle lanes
+  const int tiled = sitems >= ((size_t)1 << 20);
+  const unsigned sbk = tiled ? 2 * ((p.i + 63) / 64) * ((gs + 31) / 32) + ((p.h + 63) / 64) * ((ds + 31) / 32)
+                             : (unsigned)((sitems + 255) / 256);
+  hipLaunchKernelGGL(k_w4a4_prologue, dim3(qb + sbk), dim3(256), 0, st, p, qb, tiled);
   return hipGetLastError();
 }
 

@@ -185,6 +185,17 @@ def test_config2_fused_and_dequant(dev):
     d.free()
 
 
+def test_w4a4_ragged_scale_tiles(dev):
+    """W4A4 with more than 2^20 weight-scale dwords (the tiled stage-major
+    conversion) and stage counts that leave partial 32-stage tiles (gate/up
+    18 stages, down 157)."""
+    T, H, I = 64, 2304, 20096
+    d = MlpData(dev, T, H, I, seed=19)
+    rows = sample_rows(T, 8)
+    check(run_mlp(dev, d, M.MLP_W4A4)[rows], oracle_mlp(d, M.MLP_W4A4, rows=rows), what="W4A4 ragged tiles")
+    d.free()
+
+
 def test_config4_w4a4(dev):
     d = MlpData(dev, 4096, 8192, 28672, seed=17)
     rows = sample_rows(4096, 12)
