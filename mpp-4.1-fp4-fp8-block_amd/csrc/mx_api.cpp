@@ -155,6 +155,8 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
       s.sg = take(I * H / 32);
       s.su = take(I * H / 32);
       s.sd = take(H * I / 32);
+      s.qws = take(std::max(mx::gemm_fp4_ws_bytes(1, (int)T, (int)I, (int)H),
+                            mx::gemm_fp4_ws_bytes(0, (int)T, (int)H, (int)I)));
     } else {
       s.xs = take(T * H / 32);
       s.ms = take(T * I / 32);
@@ -240,8 +242,9 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
       uint8_t* su2 = ws + s.su;
       uint8_t* sd2 = ws + s.sd;
       mx::W4A4Prologue pro{static_cast<const uint16_t*>(x), xq, xs, sg, su, sd, sg2, su2, sd2, T, H, I};
-      mx::Fp4GemmArgs gu{xq, xs, wg, sg2, wu, su2, mq, ms, T, I, H, 1};
-      mx::Fp4GemmArgs dn{mq, ms, wd, sd2, nullptr, nullptr, out, nullptr, T, H, I, 1};
+      float* part = reinterpret_cast<float*>(ws + s.qws);
+      mx::Fp4GemmArgs gu{xq, xs, wg, sg2, wu, su2, mq, ms, T, I, H, 1, part, mx::gemm_fp4_splits(1, T, I, H)};
+      mx::Fp4GemmArgs dn{mq, ms, wd, sd2, nullptr, nullptr, out, nullptr, T, H, I, 1, part, mx::gemm_fp4_splits(0, T, H, I)};
       steps.push_back({"w4a4_prologue", [=] { return mx::launch_w4a4_prologue(pro, st); }});
       steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
       steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});

@@ -26,6 +26,10 @@
 // (the loop is unrolled by 2) and the barrier is a bare s_barrier, so the
 // backend does not turn the stage wait into vmcnt(0) for unrelated DMA.
 // Every wave issues exactly 17 DMA instructions per stage.
+//
+// Small-M plain GEMMs (too few tiles for the CUs) split K: workgroups of
+// split s run stages [s * KT/S, (s + 1) * KT/S) and store f32 partials, and a
+// second launch adds the S partials in split order and stores f16.
 #include "mx_device.h"
 #include "mx_internal.h"
 
@@ -63,7 +67,7 @@ __device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
   return (bid % 8) * per + bid / 8;
 }
 
-template <bool DUAL>
+template <bool DUAL, bool SPLIT>
 __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -74,7 +78,13 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
   const size_t Mpad = stage_major_rows(M);
   const size_t NB = (size_t)g.n;
 
-  const int tile = xcd_tile(blockIdx.x, MT * NT);
+  // Split-K: workgroup b takes split b / tiles, stages [split * KT, +KT).
+  const int tiles = MT * NT;
+  const int splits = SPLIT ? g.splits : 1;
+  const int split = SPLIT ? blockIdx.x / tiles : 0;
+  const int KT = K / kKS / splits;
+  const size_t kbeg = (size_t)split * KT;
+  const int tile = xcd_tile(blockIdx.x - split * tiles, tiles);
   const int group_sz = 8 * MT;
   const int grp = tile / group_sz, in_grp = tile % group_sz;
   const int nt_base = grp * 8;
@@ -91,12 +101,12 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
   for (int q = 0; q < 8; q++) {
     const int r = wave * 64 + q * 8 + drow;
     const int c = (lane & 7) ^ swz(r);
-    a_src[q] = g.a + (size_t)min(m0 + r, M - 1) * row_bytes + c * 16;
+    a_src[q] = g.a + (size_t)min(m0 + r, M - 1) * row_bytes + kbeg * kRowB + c * 16;
   }
   // B rows of one wave are consecutive rows of one matrix; the swizzle of
   // row 64w + 8q + l/8 is (l/8) ^ (q % 4), so four chunk offsets cover q.
-  const uint8_t* b_src = DUAL ? (wave < 2 ? g.b0 : g.b1) + (size_t)(nt * 128 + (wave & 1) * 64 + drow) * row_bytes
-                              : g.b0 + (size_t)(nt * 256 + wave * 64 + drow) * row_bytes;
+  const uint8_t* b_src = (DUAL ? (wave < 2 ? g.b0 : g.b1) + (size_t)(nt * 128 + (wave & 1) * 64 + drow) * row_bytes
+                               : g.b0 + (size_t)(nt * 256 + wave * 64 + drow) * row_bytes) + kbeg * kRowB;
   int b_co[4];
 #pragma unroll
   for (int q = 0; q < 4; q++) b_co[q] = ((lane & 7) ^ swz(wave * 64 + q * 8 + drow)) * 16;
@@ -114,6 +124,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
     s_src = g.s0 + ((size_t)(wave - 2) * NB + nt * 256 + 4 * lane) * 4;
     s_plane = NB * 4;
   }
+  s_src += kbeg * 2 * s_plane;
 
   // ---- operand reads.  k-step s, lane half h = lane / 32 -> chunk 2s + h.
   int bfrag[4];
@@ -142,7 +153,6 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
 
   v4i af[2][4], bf[2][4];
   uint32_t sa[2][2][4], sb[2][2][4];  // [stage parity][plane][block]
-  const int KT = K / kKS;
 
 #define MX5_ISSUE(S, SP)                                                                          \
   {                                                                                               \
@@ -235,6 +245,25 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
+  if (SPLIT) {
+    // f32 partials [split][M][N]
+    static_assert(!(DUAL && SPLIT), "the dual epilogue needs the whole K sum");
+    const size_t plane = (size_t)M * g.n;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int col = nt * 256 + (wn * 4 + j) * 32 + r32;
+        float* dst = g.ws + (size_t)split * plane + col;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int row = m0 + wm * 128 + i * 32 + acc32_row(lane, v);
+          if (row < M) dst[(size_t)row * g.n] = acc[i][j][v];
+        }
+      }
+    return;
+  }
+
   if (!DUAL) {
     uint16_t* c = reinterpret_cast<uint16_t*>(g.c);
 #pragma unroll
@@ -293,15 +322,64 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
   }
 }
 
+// Split-K reduce, plain epilogue: 4 consecutive outputs per thread, the
+// splits summed in order 0, 1, ... in f32, stored as f16.
+__global__ __launch_bounds__(256) void k_fp4_reduce_f16(Fp4GemmArgs g) {
+  const size_t plane = (size_t)g.m * g.n;
+  const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (o >= plane) return;
+  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = 0; k < g.splits; k++) {
+    const float4 v = *reinterpret_cast<const float4*>(g.ws + (size_t)k * plane + o);
+    s[0] += v.x; s[1] += v.y; s[2] += v.z; s[3] += v.w;
+  }
+  uint2 h;
+  h.x = f32_to_f16_bits(s[0]) | ((uint32_t)f32_to_f16_bits(s[1]) << 16);
+  h.y = f32_to_f16_bits(s[2]) | ((uint32_t)f32_to_f16_bits(s[3]) << 16);
+  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.c) + o) = h;
+}
+
 }  // namespace
 
 bool gemm_fp4_v5_ok(int k) { return k % (2 * kKS) == 0; }
 
+// Splits for the small-M plain GEMMs whose tiles alone leave most CUs idle
+// (one workgroup per CU: the ring takes 136 KB of LDS): double while the
+// grid stays within 256 workgroups and every split keeps an even number
+// (>= 2) of 256-K stages.  At M=128, N=1024, K=4096 (4 tiles, 16 stages) 8
+// splits take the GEMM from 29 us to about 17 us with the reduce.  The dual
+// gate/up GEMM is not split: its partials are two planes and its reduce
+// carries the SwiGLU + requantize epilogue, and at M=128, N=4096, K=1024 two
+// splits measured 8 us slower than none.
+int gemm_fp4_splits(int dual, int m, int n, int k) {
+  if (dual || !gemm_fp4_v5_ok(k)) return 1;
+  const int tiles = ((m + kM - 1) / kM) * (dual ? n / 128 : n / 256);
+  const int kt = k / kKS;
+  int s = 1;
+  while (tiles * 2 * s <= 256 && kt % (4 * s) == 0) s *= 2;
+  return s;
+}
+
+size_t gemm_fp4_ws_bytes(int dual, int m, int n, int k) {
+  const int s = gemm_fp4_splits(dual, m, n, k);
+  return s > 1 ? (size_t)s * (dual ? 2 : 1) * m * n * 4 : 0;
+}
+
 hipError_t launch_gemm_fp4_v5(int dual, const Fp4GemmArgs& g, hipStream_t st) {
   const int MT = (g.m + kM - 1) / kM;
   const int NT = dual ? g.n / 128 : g.n / 256;
-  if (dual) hipLaunchKernelGGL(k_gemm_fp4_v5<true>, dim3(MT * NT), dim3(256), 0, st, g);
-  else hipLaunchKernelGGL(k_gemm_fp4_v5<false>, dim3(MT * NT), dim3(256), 0, st, g);
+  const int splits = g.splits > 1 ? g.splits : 1;
+  if (splits > 1 && (dual || !g.ws || (g.k / kKS) % (2 * splits))) return hipErrorInvalidValue;
+  const dim3 grid(MT * NT * splits);
+  if (splits > 1) {
+    hipLaunchKernelGGL((k_gemm_fp4_v5<false, true>), grid, dim3(256), 0, st, g);
+    const size_t threads = (size_t)g.m * g.n / 4;
+    hipLaunchKernelGGL(k_fp4_reduce_f16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, g);
+  } else if (dual) {
+    hipLaunchKernelGGL((k_gemm_fp4_v5<true, false>), grid, dim3(256), 0, st, g);
+  } else {
+    hipLaunchKernelGGL((k_gemm_fp4_v5<false, false>), grid, dim3(256), 0, st, g);
+  }
   return hipGetLastError();
 }
 

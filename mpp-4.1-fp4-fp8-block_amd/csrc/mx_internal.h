@@ -140,8 +140,14 @@ struct Fp4GemmArgs {
   uint8_t* cs;                            // mid scales (dual epilogue)
   int m, n, k;
   int stage_major;                        // 1: all scale planes stage-major
+  float* ws;                              // split-K partials (splits > 1)
+  int splits;                             // K splits, from gemm_fp4_splits (0 or 1: none)
 };
 hipError_t launch_gemm_fp4(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+// K splits for the W4A4 GEMM of this shape (stage-major scales) and the
+// bytes of f32 partials they need (0 without a split).
+int gemm_fp4_splits(int dual_requant, int m, int n, int k);
+size_t gemm_fp4_ws_bytes(int dual_requant, int m, int n, int k);
 // 256x256-tile kernel for stage-major scales (mx_gemm_fp4_v3.hip).
 hipError_t launch_gemm_fp4_v3(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
 // Same with a 4-slot LDS ring (mx_gemm_fp4_v4.hip), for K % 512 == 0.

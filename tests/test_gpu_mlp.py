@@ -116,10 +116,17 @@ def test_mlp_dequant_small(dev, T):
 
 # hidden % 256 == 0 runs the stage-major 256x256 kernels; (96, 640, 1152)
 # takes the 256x128 kernels that read the reference scale layout directly.
-@pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (256, 1024, 2048), (300, 768, 1536), (96, 640, 1152)])
+# Split-K of the down GEMM (f32 partials + reduce launch) on the stage-major
+# path: (64, 512, 1024) in 2 splits, (256, 1024, 2048) in 4, (130, 1024,
+# 4096) in 8 with a ragged last tile row.
+@pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (256, 1024, 2048), (300, 768, 1536), (96, 640, 1152),
+                                   (130, 1024, 4096)])
 def test_mlp_w4a4_small(dev, T, H, I):
     d = MlpData(dev, T, H, I, seed=200 + T)
-    check(run_mlp(dev, d, M.MLP_W4A4), oracle_mlp(d, M.MLP_W4A4), what=f"w4a4 T={T}")
+    got = run_mlp(dev, d, M.MLP_W4A4)
+    check(got, oracle_mlp(d, M.MLP_W4A4), what=f"w4a4 T={T}")
+    # deterministic (split-K partials are added in a fixed order)
+    assert np.array_equal(run_mlp(dev, d, M.MLP_W4A4).view(np.uint16), got.view(np.uint16))
     d.free()
 
 
