@@ -610,10 +610,14 @@ using namespace qgemm;
 // tiles alone do not, keeping at least 8 stages per split (shorter splits
 // lose more to the partial-sum round trip and the reduce launch than they
 // gain in parallelism: the dual gate/up GEMM at M=128, N=4096, K=1024,
-// 16 stages, runs 14.9 us at two splits against 17.4 us at four).
+// 16 stages, runs 14.9 us at two splits against 17.4 us at four).  From 192
+// tiles on (three quarters of the CUs busy without a split) K is not split:
+// the f32 partials would move more bytes than the weights (W8A8 at M=128,
+// N=2x14336, K=4096: 80 -> 72 us for the MLP without the split).
 int gemm_q_splits(int ak, int epi, int m, int n, int k) {
   const int tiles = ((m + kTM - 1) / kTM) * (is_dual(epi) ? n / 64 : (n % 128 == 0 ? n / 128 : n / 64));
   const int kt = k / stage_k(ak);
+  if (tiles >= 192) return 1;
   int s = 1;
   while (tiles * s < 384 && kt % (2 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
   return s;
