@@ -34,7 +34,9 @@ class MoeData:
             self.mats.append((q, s, n, k))
         self.weights = M.Device.weights(*[(q, s) for q, s, _, _ in self.mats])
 
-    def oracle(self):
+    def oracle(self, rows=None):
+        """Oracle MLP of every expert on its rows; `rows` (token indices)
+        limits the work to those tokens (the others stay zero)."""
         x = self.dev.download(self.x, np.float16, (self.T, self.H))
         host = [(self.dev.download(q, np.uint8, (n, k // 2)), self.dev.download(s, np.uint8, (n, k // 32)))
                 for q, s, n, k in self.mats]
@@ -42,10 +44,11 @@ class MoeData:
         t0 = 0
         H, I = self.H, self.I
         for e, cnt in enumerate(self.counts):
-            if cnt:
+            sel = np.arange(t0, t0 + cnt) if rows is None else np.array([r for r in rows if t0 <= r < t0 + cnt], int)
+            if len(sel):
                 sl = lambda m, rows: (m[0][e * rows:(e + 1) * rows], m[1][e * rows:(e + 1) * rows])
                 (qg, sg), (qu, su), (qd, sd) = sl(host[0], I), sl(host[1], I), sl(host[2], H)
-                out[t0:t0 + cnt] = O.mlp_mxfp4(O.MLP_F16, x[t0:t0 + cnt], qg, sg, qu, su, qd, sd, H, I, threads=16)
+                out[sel] = O.mlp_mxfp4(O.MLP_F16, x[sel], qg, sg, qu, su, qd, sd, H, I, threads=16)
             t0 += cnt
         return out
 
@@ -100,6 +103,28 @@ def test_moe_gemm_experts(dev, counts, H, I):
     for e, cnt in enumerate(counts):
         if cnt:
             check(got[t0:t0 + cnt], ref[t0:t0 + cnt], f"expert {e} ({cnt} tokens)")
+        t0 += cnt
+    d.free()
+
+
+def test_moe_gemm_large_groups(dev):
+    """Grouped GEMMs at a larger shape: 8 experts of up to 256 tokens
+    (two 128-row tiles, the second ragged for most experts), H=4096,
+    I=2048, 512 gate/up and 512 down workgroups.  Six sampled tokens per
+    expert are checked, the first and last among them."""
+    counts, H, I = [256, 200, 256, 130, 256, 256, 64, 256], 4096, 2048
+    d = MoeData(dev, counts, H, I, seed=91)
+    got = d.run()
+    rng = np.random.default_rng(5)
+    rows, t0 = [], 0
+    for cnt in counts:
+        rows += sorted(set([t0, t0 + cnt - 1] + list(t0 + rng.integers(0, cnt, 4))))
+        t0 += cnt
+    ref = d.oracle(rows=rows)
+    t0 = 0
+    for e, cnt in enumerate(counts):
+        sel = [r for r in rows if t0 <= r < t0 + cnt]
+        check(got[sel], ref[sel], f"expert {e} ({cnt} tokens, {len(sel)} sampled)")
         t0 += cnt
     d.free()
 
