@@ -96,9 +96,10 @@ void orc_mlp_format(int fmt, int tokens, int hidden, int inter, const uint16_t *
 /* ---- reference data generators (MS:2785-2842) --------------------------
  * lcg_bytes, lcg_pattern and lcg_half are pinned end to end by the
  * reference's published checksum 403573 (README.md:292-294), which is
- * computed over data made by all three.  lcg_int8 (makeInt8MatrixValues)
- * has no published output: parity unpinned (restated from the source only;
- * no MLP row of this build consumes it). */
+ * computed over data made by all three.  lcg_int8 (makeInt8MatrixValues,
+ * MS:2833-2842) has no published output of its own; it is makeHalfMatrixValues
+ * before the Float16 scale, and is pinned by equality with lcg_half at
+ * scale 1 (tests/test_oracle_mlp.py). */
 void orc_lcg_bytes(uint32_t seed, size_t count, uint8_t *out);
 void orc_lcg_pattern(uint32_t seed, size_t count, const uint8_t *pattern, int pattern_count,
                      uint8_t *out);
@@ -106,9 +107,10 @@ void orc_lcg_half(uint32_t seed, size_t count, float scale, uint16_t *out);
 void orc_lcg_int8(uint32_t seed, size_t count, int8_t *out);
 
 /* ---- checksums (MS:2844-2884) ------------------------------------------
- * checksum_f32 is pinned by 403573; checksum_i32 and checksum_f16raw
- * (sampleIntChecksum / the half variant) have no published value: parity
- * unpinned, the same 32-sample stride restated. */
+ * checksum_f32 is pinned by 403573.  checksum_i32 and checksum_f16raw
+ * (sampleIntChecksum / sampleHalfRawChecksum) have no published value; they
+ * sample like checksum_f32 and are pinned by equality with it on integer
+ * data and by the closed form on index ramps (tests/test_oracle_mlp.py). */
 double orc_checksum_f32(const float *p, size_t count, int *samples);
 int64_t orc_checksum_i32(const int32_t *p, size_t count, int *samples);
 uint64_t orc_checksum_f16raw(const uint16_t *p, size_t count, int *samples);

@@ -254,6 +254,13 @@ def checksum_f32(a: np.ndarray):
     return s, n.value
 
 
+def checksum_i32(a: np.ndarray):
+    a = np.ascontiguousarray(a, np.int32).reshape(-1)
+    n = _int(0)
+    s = lib().orc_checksum_i32(_p(a), a.size, ctypes.byref(n))
+    return s, n.value
+
+
 def checksum_f16raw(a: np.ndarray):
     a = np.ascontiguousarray(a).view(np.uint16).reshape(-1)
     n = _int(0)

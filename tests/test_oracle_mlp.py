@@ -44,6 +44,44 @@ def test_reference_checksum_403573():
     assert "%.6g" % s == kat["checksum"]
 
 
+def test_lcg_int8_is_lcg_half_at_unit_scale():
+    """makeInt8MatrixValues (main.swift:2833-2842) is makeHalfMatrixValues
+    (:2821-2831) before its Float16(Float(signed) * scale): same state update,
+    same signed nibble.  lcg_half is pinned by 403573 above, so lcg_int8 must
+    equal lcg_half at scale 1 exactly (-8..7 are exact in f16); a wrong
+    shift, xor, index term or seed handling breaks the equality."""
+    for seed, count in ((0, 1), (1, 33), (0x2A, 4097), (0xDEADBEEF, 70001), (0xFFFFFFFF, 1000)):
+        i8 = O.lcg_int8(seed, count)
+        h = O.lcg_half(seed, count, 1.0).astype(np.float32)
+        assert np.array_equal(i8.astype(np.float32), h), (seed, count)
+        assert i8.min() >= -8 and i8.max() <= 7
+    # every signed nibble value occurs (the top nibble of the state is used)
+    assert set(np.unique(O.lcg_int8(7, 4096))) == set(range(-8, 8))
+
+
+def test_int_and_raw_half_checksums_share_the_pinned_sampling():
+    """sampleIntChecksum and sampleHalfRawChecksum (main.swift:2858-2884)
+    sample exactly like sampleFloatChecksum (:2844-2856, pinned by 403573):
+    step max(1, count/32), from index 0.  Checked against the float checksum
+    on integer data (exact in f32 and double below 2^24) and in closed form:
+    on the ramp a[i] = i the sum is step * n(n-1)/2 with n = ceil(count/step)."""
+    rng = np.random.default_rng(12)
+    for count in (1, 5, 31, 32, 33, 64, 100, 1023, 4096, 100003):
+        step = max(1, count // 32)
+        n = -(-count // step)
+        v = rng.integers(-(1 << 20), 1 << 20, count).astype(np.int32)
+        si, ni = O.checksum_i32(v)
+        sf, nf = O.checksum_f32(v.astype(np.float32))
+        assert ni == nf == n and si == int(sf), count
+        h = rng.integers(0, 1 << 16, count).astype(np.uint16)
+        sh, nh = O.checksum_f16raw(h.view(np.float16))
+        assert nh == n and sh == O.checksum_i32(h.astype(np.int32))[0], count
+        ramp = np.arange(count, dtype=np.int32)
+        assert O.checksum_i32(ramp) == (step * n * (n - 1) // 2, n), count
+        if count <= 1 << 16:  # the raw-half ramp fits 16 bits
+            assert O.checksum_f16raw(ramp.astype(np.uint16).view(np.float16))[0] == step * n * (n - 1) // 2
+
+
 def test_quantizer_invariants():
     rng = np.random.default_rng(1)
     w = rng.normal(0, 0.02, (256, 1024)).astype(np.float32)
