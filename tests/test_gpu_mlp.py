@@ -118,9 +118,10 @@ def test_mlp_dequant_small(dev, T):
 # takes the 256x128 kernels that read the reference scale layout directly.
 # Split-K of the down GEMM (f32 partials + reduce launch) on the stage-major
 # path: (64, 512, 1024) in 2 splits, (256, 1024, 2048) in 4, (130, 1024,
-# 4096) in 8 with a ragged last tile row.
+# 4096) in 8 with a ragged last tile row, (400, 512, 2048) in 4 over two
+# row tiles (the second ragged).
 @pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (256, 1024, 2048), (300, 768, 1536), (96, 640, 1152),
-                                   (130, 1024, 4096)])
+                                   (130, 1024, 4096), (400, 512, 2048)])
 def test_mlp_w4a4_small(dev, T, H, I):
     d = MlpData(dev, T, H, I, seed=200 + T)
     got = run_mlp(dev, d, M.MLP_W4A4)
