@@ -94,7 +94,10 @@ def test_moe_decode_experts(dev, counts, H, I):
     d.free()
 
 
-@pytest.mark.parametrize("counts,H,I", [([40, 0, 200], 512, 1024), ([17, 130, 5, 64], 256, 640)])
+# (320, 576): channel counts that are multiples of 64 but not 128, so the
+# down GEMM takes its 64-row weight tiles.
+@pytest.mark.parametrize("counts,H,I", [([40, 0, 200], 512, 1024), ([17, 130, 5, 64], 256, 640),
+                                        ([20, 33, 0, 150], 320, 576)])
 def test_moe_gemm_experts(dev, counts, H, I):
     d = MoeData(dev, counts, H, I, seed=len(counts) + I)
     got = d.run()
