@@ -172,11 +172,13 @@ int mx_gemm_i8(mx_ctx* ctx, const int8_t* a, const int8_t* b, int32_t* c, int m,
 enum { MX_PROBE_F16 = 0, MX_PROBE_FP4 = 1, MX_PROBE_FP8 = 2, MX_PROBE_INT4 = 3, MX_PROBE_I8 = 4 };
 int mx_accum_gemm(mx_ctx* ctx, int a_fmt, const void* a, int b_fmt, const void* b, void* c,
                   int c_dtype, int m, int n, int k);
-/* SwiGLU: variant 0 mpp_mlp_swiglu_float, 1 mpp_mlp_swiglu_half,
- * 2 mpp_mlp_swiglu_half_from_half, 3 mpp_mlp_swiglu_i8
- * (MPPMLPKernels.metal:186-257; ABI gate, up, mid, config). */
-int mx_swiglu(mx_ctx* ctx, int variant, const void* gate, const void* up, void* mid, int tokens,
-              int intermediate);
+/* SwiGLU over cfg->tokens x cfg->intermediate elements, in the Metal
+ * kernels' buffer order gate, up, mid, MLPConfig (MPPMLPKernels.metal:186-257),
+ * then the kernel choice: variant 0 mpp_mlp_swiglu_float (f32 -> f32),
+ * 1 mpp_mlp_swiglu_half (f32 -> f16), 2 mpp_mlp_swiglu_half_from_half
+ * (f16 -> f16), 3 mpp_mlp_swiglu_i8 (i32 -> i8). */
+int mx_swiglu(mx_ctx* ctx, const void* gate, const void* up, void* mid, const mx_mlp_config* cfg,
+              int variant);
 
 /* ---- MLP ------------------------------------------------------------------ */
 /* down(silu(gate(x)) * up(x)).  x f16 [T][H]; weights MXFP4; out f16 [T][H]

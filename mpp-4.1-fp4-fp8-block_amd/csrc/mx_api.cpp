@@ -54,6 +54,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int ensure_ws(mx_ctx* c, size_t bytes) {
   if (bytes <= c->ws_bytes) return MX_OK;
+  // Growing frees the old workspace, which a graph captured earlier may
+  // still point at, and synchronises, which a capturing stream refuses.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(c->stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+    return set_err(c, MX_EINVAL,
+                   "The workspace must grow to %zu bytes, which is not allowed while the stream is being "
+                   "captured: run one forward of the largest shape before capturing.", bytes);
   if (c->ws) {
     MX_HIP(c, hipStreamSynchronize(c->stream));
     MX_HIP(c, hipFree(c->ws));
@@ -248,12 +255,18 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
       steps.push_back({"w4a4_prologue", [=] { return mx::launch_w4a4_prologue(pro, st); }});
       steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
       steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});
+      steps.push_back({"w4a4_down_inf", [=] {
+                         return mx::launch_w4a4_down_inf(wd, sd, mq, ms, 1, T, H, I, static_cast<uint16_t*>(out), st);
+                       }});
     } else {
       mx::Fp4GemmArgs gu{xq, xs, wg, sg, wu, su, mq, ms, T, I, H, 0};
       mx::Fp4GemmArgs dn{mq, ms, wd, sd, nullptr, nullptr, out, nullptr, T, H, I, 0};
       steps.push_back({"w4a4_prologue", [=] { return mx::launch_mxfp4_quantize(x, MX_DTYPE_F16, xq, xs, T, H, st); }});
       steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
       steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});
+      steps.push_back({"w4a4_down_inf", [=] {
+                         return mx::launch_w4a4_down_inf(wd, sd, mq, ms, 0, T, H, I, static_cast<uint16_t*>(out), st);
+                       }});
     }
   }
   return MX_OK;
@@ -625,13 +638,13 @@ int mx_accum_gemm(mx_ctx* c, int a_fmt, const void* a, int b_fmt, const void* b,
   return run_gemm(c, pa, MX_DTYPE_F16, bk, pb, sc, out, epi, m, n, (int)kp, a_sz + b_sz + plane);
 }
 
-int mx_swiglu(mx_ctx* c, int variant, const void* gate, const void* up, void* mid, int tokens,
-              int intermediate) {
+int mx_swiglu(mx_ctx* c, const void* gate, const void* up, void* mid, const mx_mlp_config* cfg, int variant) {
   if (!c) return MX_EINVAL;
   if (variant < 0 || variant > 3) return set_err(c, MX_EINVAL, "Unknown SwiGLU variant %d.", variant);
-  if (tokens <= 0 || intermediate <= 0) return set_err(c, MX_EINVAL, "SwiGLU sizes must be positive.");
+  if (!cfg) return set_err(c, MX_EINVAL, "MLP config is null.");
+  if (cfg->tokens == 0 || cfg->intermediate == 0) return set_err(c, MX_EINVAL, "SwiGLU sizes must be positive.");
   if (!gate || !up || !mid) return set_err(c, MX_EINVAL, "SwiGLU buffers must not be null.");
-  MX_HIP(c, mx::launch_swiglu(variant, gate, up, mid, (size_t)tokens * intermediate, c->stream));
+  MX_HIP(c, mx::launch_swiglu(variant, gate, up, mid, (size_t)cfg->tokens * cfg->intermediate, c->stream));
   return MX_OK;
 }
 
@@ -650,14 +663,14 @@ const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index)
   static const char* ref[] = {"gemm_q_mxfp4_gate_up_swiglu_half", "gemm_q_mxfp4_down_f32"};
   static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
                               "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
-  static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down"};
+  static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down", "w4a4_down_inf"};
   if (index < 0 || !cfg || variant < MX_MLP_FUSED || variant > MX_MLP_REFROW) return nullptr;
   switch (mlp_path(variant, cfg)) {
     case PATH_GEMV: return index < 2 ? gemv[index] : nullptr;
     case PATH_GEMM_Q: return index < 2 ? fused[index] : nullptr;
     case PATH_REFROW: return index < 2 ? ref[index] : nullptr;
     case PATH_DEQUANT: return index < 7 ? deq[index] : nullptr;
-    case PATH_W4A4: return index < 3 ? w4[index] : nullptr;
+    case PATH_W4A4: return index < 4 ? w4[index] : nullptr;
   }
   return nullptr;
 }

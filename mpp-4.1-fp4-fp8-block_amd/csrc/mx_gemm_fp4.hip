@@ -273,6 +273,76 @@ static hipError_t launch_bn(const Fp4GemmArgs& g, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// E8M0 byte 255 in a down-weight scale.  The reference decodes it as +inf
+// (bits << 23, MXFP4Kernels.metal:26-29), so in its dequantize-then-
+// accumulate a block with that scale contributes +-inf when every weight
+// code of the block and every mid value it meets are non-zero and all those
+// products share one sign, and NaN otherwise (0 * inf, or +inf + -inf).
+// The scaled MFMA reads 255 as NaN, so the down GEMM leaves NaN in every
+// output of such a row.  This pass rewrites the +-inf cases.  One workgroup
+// per 16 down rows reads their scale bytes and returns when none is 255 -
+// the whole cost in the common case is one read of the down scale plane.
+// (Byte 255 in a gate or up scale needs no pass: the channel's mid is then
+// non-finite on both sides, its block re-quantizes to byte 255 with zero
+// codes, and every output of the token is NaN on both sides.)
+// ms_stage_major: mid scales [I/128][tpad][4] bytes, else [T][I/32].
+__global__ __launch_bounds__(256) void k_w4a4_down_inf(const uint8_t* __restrict__ wd, const uint8_t* __restrict__ sd,
+                                                      const uint8_t* __restrict__ mq, const uint8_t* __restrict__ ms,
+                                                      int ms_stage_major, int tpad, uint16_t* __restrict__ out,
+                                                      int T, int H, int I) {
+  const int KB = I / 32, r0 = blockIdx.x * 16;
+  const int rows = min(16, H - r0);
+  __shared__ int any;
+  if (threadIdx.x == 0) any = 0;
+  __syncthreads();
+  bool hit = false;
+  for (int i = threadIdx.x; i < rows * (KB / 4); i += blockDim.x) {
+    const uint32_t d = ~*reinterpret_cast<const uint32_t*>(sd + (size_t)(r0 + i / (KB / 4)) * KB + (i % (KB / 4)) * 4);
+    hit = hit || ((d - 0x01010101u) & ~d & 0x80808080u) != 0;
+  }
+  if (hit) any = 1;  // every writer stores the same value
+  __syncthreads();
+  if (!any) return;  // workgroup-uniform
+  auto mid_scale = [&](int m, int b) -> uint32_t {
+    return ms_stage_major ? ms[((size_t)(b >> 2) * tpad + m) * 4 + (b & 3)] : ms[(size_t)m * KB + b];
+  };
+  for (int rr = 0; rr < rows; rr++) {
+    const int h = r0 + rr;
+    const uint8_t* srow = sd + (size_t)h * KB;
+    const uint8_t* wrow = wd + (size_t)h * (I / 2);
+    for (int m = threadIdx.x; m < T; m += blockDim.x) {
+      bool inf_row = false, finite = true;
+      uint32_t sign = 0, seen = 0;  // seen: 1 = a positive, 2 = a negative infinite product
+      for (int b = 0; b < KB && finite; b++) {
+        if (mid_scale(m, b) == 255u) finite = false;  // mid not finite: NaN on both sides
+        if (srow[b] != 255u) continue;
+        inf_row = true;
+        const uint8_t* mrow = mq + (size_t)m * (I / 2) + b * 16;
+        for (int j = 0; j < 16 && finite; j++) {
+          const uint32_t wb = wrow[b * 16 + j], mb = mrow[j];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; h2++) {
+            const uint32_t wc = (wb >> (4 * h2)) & 15u, mc = (mb >> (4 * h2)) & 15u;
+            if ((wc & 7u) == 0 || (mc & 7u) == 0) finite = false;  // 0 * inf
+            sign = (wc ^ mc) & 8u;
+            seen |= sign ? 2u : 1u;
+          }
+        }
+      }
+      if (inf_row && finite && seen != 3u) out[(size_t)m * H + h] = seen == 2u ? 0xfc00u : 0x7c00u;
+    }
+  }
+}
+
+hipError_t launch_w4a4_down_inf(const uint8_t* wd, const uint8_t* sd, const uint8_t* mq, const uint8_t* ms,
+                                int ms_stage_major, int t, int h, int i, uint16_t* out, hipStream_t st) {
+  const int tpad = (int)stage_major_rows(t);
+  hipLaunchKernelGGL(k_w4a4_down_inf, dim3((h + 15) / 16), dim3(256), 0, st, wd, sd, mq, ms, ms_stage_major, tpad,
+                     out, t, h, i);
+  return hipGetLastError();
+}
+
 // Preconditions (caller): k % 128 == 0; DUAL: n % 64 == 0; else n % 128 == 0.
 // Stage-major scale planes go to the 256 x 256 streaming kernel
 // (mx_gemm_fp4_v3.hip); reference-layout planes to the kernel above.

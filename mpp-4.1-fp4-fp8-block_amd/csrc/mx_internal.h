@@ -168,5 +168,10 @@ struct W4A4Prologue {
   int t, h, i;
 };
 hipError_t launch_w4a4_prologue(const W4A4Prologue& p, hipStream_t st);
+// After the W4A4 down GEMM: outputs of rows whose down scales hold byte 255
+// rewritten to the reference's +-inf where its semantics give infinity
+// (mid codes mq [T][I/2], mid scales stage-major or [T][I/32]).
+hipError_t launch_w4a4_down_inf(const uint8_t* wd, const uint8_t* sd, const uint8_t* mq, const uint8_t* ms,
+                                int ms_stage_major, int t, int h, int i, uint16_t* out, hipStream_t st);
 
 }  // namespace mx

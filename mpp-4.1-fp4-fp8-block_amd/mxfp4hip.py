@@ -109,7 +109,7 @@ def load() -> ctypes.CDLL:
         "mx_gemm_f16": (_int, [_vp, _vp, _int, _vp, _vp, _int, _int, _int]),
         "mx_gemm_i8": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int]),
         "mx_accum_gemm": (_int, [_vp, _int, _vp, _int, _vp, _vp, _int, _int, _int, _int]),
-        "mx_swiglu": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int]),
+        "mx_swiglu": (_int, [_vp, _vp, _vp, _vp, P(MlpConfig), _int]),
         "mx_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp, _int,
                                     _int, _int, P(ctypes.c_double), P(ctypes.c_double), P(_int)]),
@@ -278,7 +278,10 @@ class Device:
         self._check(load().mx_accum_gemm(self.ctx, a_fmt, a.p, b_fmt, b.p, c.p, c_dtype, m, n, k))
 
     def swiglu(self, variant, gate: DevBuf, up: DevBuf, mid: DevBuf, tokens, inter):
-        self._check(load().mx_swiglu(self.ctx, variant, gate.p, up.p, mid.p, tokens, inter))
+        """mx_swiglu: gate, up, mid, MLPConfig, then the variant (0 float,
+        1 half, 2 half from half, 3 i8)."""
+        cfg = MlpConfig(tokens, 0, inter)
+        self._check(load().mx_swiglu(self.ctx, gate.p, up.p, mid.p, ctypes.byref(cfg), variant))
 
     def fill_normal(self, buf: DevBuf, dtype: int, n: int, seed: int, mean=0.0, std=1.0):
         self._check(load().mx_fill_normal(self.ctx, buf.p, dtype, n, seed, mean, std))

@@ -354,6 +354,21 @@ void orc_swiglu_half(const float *gate, const float *up, size_t count, uint16_t 
     }
 }
 
+/* mpp_mlp_swiglu_i8 (MP:240-257): g = clamp(gate * 2^-12, +-20),
+ * u = up * 2^-12 (not clamped), v = silu(g) * u * 32, mid = int8(rint(clamp(v,
+ * -128, 127))).  rintf rounds half to even, as Metal's rint does. */
+void orc_swiglu_i8(const int32_t *gate, const int32_t *up, size_t count, int8_t *mid)
+{
+    for (size_t i = 0; i < count; i++) {
+        float g = (float)gate[i] * 0.000244140625f;
+        g = g < -20.0f ? -20.0f : (g > 20.0f ? 20.0f : g);
+        float u = (float)up[i] * 0.000244140625f;
+        float v = orc_silu(g) * u * 32.0f;
+        v = v < -128.0f ? -128.0f : (v > 127.0f ? 127.0f : v);
+        mid[i] = (int8_t)(int)rintf(v);
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Threaded row loops.  Work is split over weight rows; each worker decodes a
  * row once and dots it with every selected token. */

@@ -62,6 +62,7 @@ void orc_mxfp4_matmul(const void *a, int a_kind, const uint8_t *b, const uint8_t
 float orc_silu(float g);
 void orc_swiglu_float(const float *gate, const float *up, size_t count, float *mid);   /* MP:186-202 */
 void orc_swiglu_half(const float *gate, const float *up, size_t count, uint16_t *mid); /* MP:204-220 */
+void orc_swiglu_i8(const int32_t *gate, const int32_t *up, size_t count, int8_t *mid);  /* MP:240-257 */
 
 /* ---- full MXFP4 MLP ----------------------------------------------------- */
 /* mode 0: f16 activations, dequantize-then-FP32(here: double)-accumulate,

@@ -61,6 +61,7 @@ def lib() -> ctypes.CDLL:
             "orc_silu": (ctypes.c_float, [ctypes.c_float]),
             "orc_swiglu_float": (None, [_vp, _vp, _sz, _vp]),
             "orc_swiglu_half": (None, [_vp, _vp, _sz, _vp]),
+            "orc_swiglu_i8": (None, [_vp, _vp, _sz, _vp]),
             "orc_mlp_mxfp4": (None, [_int, _int, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _int, _vp, _int]),
             "orc_quant_rowwise": (None, [_int, _vp, _int, _int, _vp, _vp]),
@@ -161,6 +162,15 @@ def swiglu_half(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     out = np.empty(g.shape, np.uint16)
     lib().orc_swiglu_half(_p(g), _p(u), g.size, _p(out))
     return out.view(np.float16)
+
+
+def swiglu_i8(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """mpp_mlp_swiglu_i8 (MPPMLPKernels.metal:240-257): int32 gate/up -> int8 mid."""
+    g = np.ascontiguousarray(g, np.int32)
+    u = np.ascontiguousarray(u, np.int32)
+    out = np.empty(g.shape, np.int8)
+    lib().orc_swiglu_i8(_p(g), _p(u), g.size, _p(out))
+    return out
 
 
 MLP_F16, MLP_W4A4, MLP_REFROW = 0, 1, 2

@@ -82,6 +82,26 @@ def test_swiglu_variants(dev):
                                want2.astype(np.float32), rtol=1e-3, atol=1e-6)
 
 
+def test_swiglu_i8(dev):
+    """Variant 3, mpp_mlp_swiglu_i8 (MPPMLPKernels.metal:240-257): int32 gate
+    and up -> int8 mid, against the oracle.  Equal except where the two
+    sides' exp differ in the last bit at an exact rounding midpoint (then
+    by one); the closed-form cases (gate >= 20 * 4096) are exact."""
+    rng = np.random.default_rng(8)
+    T, I = 16, 1024
+    g = rng.integers(-120000, 120000, (T, I)).astype(np.int32)
+    u = rng.integers(-40000, 40000, (T, I)).astype(np.int32)
+    g[0, :64] = 81920 + rng.integers(0, 1 << 20, 64)
+    u[0, :64] = np.arange(-32, 32) * 16
+    dg, du = dev.upload(g), dev.upload(u)
+    mid = dev.alloc(T * I)
+    dev.swiglu(3, dg, du, mid, T, I)
+    got = dev.download(mid, np.int8, (T, I)).astype(np.int64)
+    want = O.swiglu_i8(g, u).astype(np.int64)
+    assert np.array_equal(got[0, :64], want[0, :64])
+    assert np.abs(got - want).max() <= 1 and (got != want).mean() < 1e-3
+
+
 def run_mlp(dev, d: MlpData, variant):
     out = dev.alloc(d.T * d.H * 4)
     dev.mlp_forward(variant, d.T, d.H, d.I, d.x, d.weights, out)
@@ -97,7 +117,7 @@ def oracle_mlp(d: MlpData, variant, rows=None):
     return O.mlp_mxfp4(mode, x, qg, sg, qu, su, qd, sd, d.H, d.I, rows=rows, threads=16)
 
 
-@pytest.mark.parametrize("T", [1, 2, 8, 16, 17, 64, 128])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 8, 16, 17, 64, 128])
 def test_mlp_fused_small(dev, T):
     d = MlpData(dev, T, 512, 1024, seed=T)
     got = run_mlp(dev, d, M.MLP_FUSED)
@@ -285,3 +305,123 @@ def test_decode_back_to_back_distinct_inputs(dev):
         o.free()
     a.free()
     b.free()
+
+
+def test_decode_many_launches(dev):
+    """The decode MLP over rotated weight sets, 200 forwards from one captured
+    graph (the benchmark's form) and 200 from the stream, then one forward
+    per set checked against the oracle: the shared mid buffer and the graph
+    replays leave every later forward correct."""
+    T, H, I = 1, 1024, 2048
+    sets = [MlpData(dev, T, H, I, seed=500 + s) for s in range(4)]
+    out = dev.alloc(T * H * 2)
+    dev.mlp_benchmark(M.MLP_FUSED, T, H, I, sets[0].x, [d.weights for d in sets], out, warmup=2,
+                      iterations=200, per_kernel=False, graph=True)
+    dev.mlp_benchmark(M.MLP_FUSED, T, H, I, sets[0].x, [d.weights for d in sets], out, warmup=0,
+                      iterations=200, per_kernel=False, graph=False)
+    for d in sets:
+        check(run_mlp(dev, d, M.MLP_FUSED), oracle_mlp(d, M.MLP_FUSED), what="after many launches")
+        d.free()
+    out.free()
+
+
+@pytest.mark.parametrize("T,H,I", [(1, 512, 1024), (3, 1024, 2048)])
+def test_decode_nonfinite_activations(dev, T, H, I):
+    """An inf or NaN activation propagates through the decode path as through
+    the reference's dequantize-then-accumulate: the outputs are non-finite
+    where the oracle's are and within tolerance elsewhere."""
+    d = MlpData(dev, T, H, I, seed=71 + T)
+    x = dev.download(d.x, np.float16, (T, H))
+    x[0, 5] = np.inf
+    x[T - 1, H - 3] = np.nan if T > 1 else x[T - 1, H - 3]
+    dev.upload(x, d.x)
+    got = run_mlp(dev, d, M.MLP_FUSED).astype(np.float64)
+    ref = oracle_mlp(d, M.MLP_FUSED)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    if fin.any():
+        rel, cos = O.mlp_error(got[fin], ref[fin])
+        assert rel <= TOL and cos >= COS, (rel, cos)
+    d.free()
+
+
+def _plant_e8m0(dev, d, which, rows_255, row_0):
+    q, s, n, k = d.mats[{"gate": 0, "up": 1, "down": 2}[which]]
+    sc = dev.download(s, np.uint8, (n, k // 32))
+    for r, b in rows_255:
+        if b is None:
+            sc[r, :] = 255
+        else:
+            sc[r, b] = 255
+    sc[row_0, 0] = 0
+    dev.upload(sc, s)
+
+
+def _check_nonfinite_pattern(got, ref, what):
+    got = got.astype(np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), what
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)), what
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref)), what
+    fin = np.isfinite(ref)
+    if fin.any():
+        rel, cos = O.mlp_error(got[fin], ref[fin])
+        assert rel <= TOL and cos >= COS, (what, rel, cos)
+
+
+@pytest.mark.parametrize("variant", [M.MLP_FUSED, M.MLP_DEQUANT])
+@pytest.mark.parametrize("which", ["gate", "down"])
+def test_e8m0_endpoints_tiled_paths(dev, variant, which):
+    """E8M0 bytes 255 (+inf in the reference, MXFP4Kernels.metal:26-29) and
+    0 (0.0) on the tiled small-M GEMM (fused, T > 16) and on the
+    dequant-to-half path: non-finite outputs where the oracle has them,
+    tolerance elsewhere."""
+    T, H, I = 40, 512, 1024
+    d = MlpData(dev, T, H, I, seed=131 + variant)
+    _plant_e8m0(dev, d, which, [(3, 2), (I - 1 if which != "down" else H - 1, None)], 100)
+    got = run_mlp(dev, d, variant)
+    ref = oracle_mlp(d, variant)
+    assert np.isnan(ref).any() or np.isinf(ref).any()
+    _check_nonfinite_pattern(got, ref, f"variant {variant} {which}")
+    d.free()
+
+
+@pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (96, 640, 1152)])
+@pytest.mark.parametrize("which", ["up", "down"])
+def test_e8m0_endpoints_w4a4(dev, T, H, I, which):
+    """W4A4 (both scale layouts): byte 255 in an up scale makes the channel's
+    mid non-finite on both sides, so every output of those tokens is NaN;
+    in a down scale the scaled MFMA's NaN is rewritten to the reference's
+    +-inf where every product of the block is an infinity of one sign.  A
+    down row whose codes are all non-zero and positive, met by a token whose
+    mid codes there are too, must come out +inf.  Byte 0 (0.0 in the
+    reference, 2^-127 in hardware) stays within tolerance."""
+    d = MlpData(dev, T, H, I, seed=151 + T)
+    if which == "up":
+        _plant_e8m0(dev, d, "up", [(5, 1)], 17)
+    else:
+        # token 0 meets down row 7 with an infinite scale on block 3 (mid
+        # channels 96..127) through all-positive, non-zero products: x row 0
+        # positive, gate/up rows 96..127 and down row 7 all code +1.0, so
+        # mid[0][96..127] are equal positive values -> +inf in the reference
+        x = dev.download(d.x, np.float16, (T, H))
+        x[0] = np.abs(x[0]) + np.float16(0.25)
+        dev.upload(x, d.x)
+        for j in (0, 1):
+            q, _, n, k = d.mats[j]
+            codes = dev.download(q, np.uint8, (n, k // 2))
+            codes[96:128, :] = 0x22
+            dev.upload(codes, q)
+        q, _, n, k = d.mats[2]
+        codes = dev.download(q, np.uint8, (n, k // 2))
+        codes[7, :] = 0x22
+        dev.upload(codes, q)
+        _plant_e8m0(dev, d, "down", [(7, 3), (H - 1, None), (11, 0)], 17)
+    got = run_mlp(dev, d, M.MLP_W4A4)
+    ref = oracle_mlp(d, M.MLP_W4A4)
+    assert (~np.isfinite(ref)).any()
+    if which == "down":
+        assert np.isposinf(ref[0, 7]), ref[0, 7]
+    _check_nonfinite_pattern(got, ref, f"w4a4 {which} T={T} H={H} I={I}")
+    d.free()
