@@ -708,11 +708,13 @@ static int time_passes(mx_ctx* c, const std::vector<std::vector<Step>>& sets, in
       return set_err(c, MX_EGPU, "graph launch failed");
     }
   }
-  hipEvent_t e0, e1;
-  MX_HIP(c, hipEventCreate(&e0));
-  MX_HIP(c, hipEventCreate(&e1));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = MX_OK;
   do {
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+      rc = set_err(c, MX_EGPU, "event create failed");
+      break;
+    }
     if (hipStreamSynchronize(c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "sync failed"); break; }
     if (hipEventRecord(e0, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
     if (gexec) {
@@ -727,8 +729,8 @@ static int time_passes(mx_ctx* c, const std::vector<std::vector<Step>>& sets, in
     (void)hipEventElapsedTime(&ms, e0, e1);
     *seconds = ms / 1000.0;
   } while (0);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
   if (gexec) (void)hipGraphExecDestroy(gexec);
   return rc;
 }

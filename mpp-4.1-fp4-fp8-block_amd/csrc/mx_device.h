@@ -4,8 +4,8 @@
 //   data   [N][K/2] bytes, two E2M1 codes per byte, low nibble = even k
 //   scales [N][K/32] E8M0 bytes, value 2^(byte-127)
 //
-// MFMA operand layouts used below (checked on gfx950 by the lane-layout
-// tests in tests/test_gpu_mfma_layout.py):
+// MFMA operand layouts used below (each kernel's GPU parity tests against
+// the oracle would fail on a wrong lane layout):
 //   v_mfma_scale_f32_32x32x64_f8f6f4 (fp4): lane l holds row l%32,
 //       k = 32*(l/32) + j, j = nibble j of 4 dwords (low nibble first);
 //       the lane's scale byte applies to exactly that (row, 32-k block).

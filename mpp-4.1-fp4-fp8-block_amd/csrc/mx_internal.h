@@ -150,9 +150,6 @@ int gemm_fp4_splits(int dual_requant, int m, int n, int k);
 size_t gemm_fp4_ws_bytes(int dual_requant, int m, int n, int k);
 // 256x256-tile kernel for stage-major scales (mx_gemm_fp4_v3.hip).
 hipError_t launch_gemm_fp4_v3(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
-// Same with a 4-slot LDS ring (mx_gemm_fp4_v4.hip), for K % 512 == 0.
-hipError_t launch_gemm_fp4_v4(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
-bool gemm_fp4_v4_ok(int k);
 // Full-cache-line DMA, K stage 256 (mx_gemm_fp4_v5.hip), for K % 512 == 0.
 hipError_t launch_gemm_fp4_v5(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
 bool gemm_fp4_v5_ok(int k);

@@ -15,6 +15,10 @@
 // {...}}, then the data region (offsets are relative to its start).
 #include <hip/hip_runtime.h>
 
+#include <cerrno>
+#include <climits>
+#include <cstdlib>
+
 #include <cctype>
 #include <cstdio>
 #include <cstring>
@@ -101,12 +105,19 @@ class Json {
     }
     return eat('"');
   }
+  // The header is untrusted: a value outside long long fails the parse
+  // (strtoll with an errno check) instead of throwing across the C ABI.
   bool integer(long long* v) {
     const size_t start = pos_;
     if (peek() == '-') pos_++;
     while (std::isdigit((unsigned char)peek())) pos_++;
-    if (pos_ == start) return ok_ = false;
-    *v = std::stoll(s_.substr(start, pos_ - start));
+    if (pos_ == start || (pos_ == start + 1 && s_[start] == '-')) return ok_ = false;
+    const std::string digits = s_.substr(start, pos_ - start);
+    errno = 0;
+    char* endp = nullptr;
+    const long long r = std::strtoll(digits.c_str(), &endp, 10);
+    if (errno == ERANGE || endp != digits.c_str() + digits.size()) return ok_ = false;
+    *v = r;
     return true;
   }
   bool int_array(std::vector<long long>* out) {
@@ -305,7 +316,8 @@ int mx_load_mxfp4(mx_ctx* ctx, const char* path, const char* blocks_name, const 
   const size_t lead = s.shape.size() - 2;
   const long long n = s.shape[lead], kb = s.shape[lead + 1];
   long long count = 1;
-  for (size_t i = 0; i < lead; i++) count *= s.shape[i];
+  bool overflow = false;
+  for (size_t i = 0; i < lead; i++) overflow = overflow || __builtin_mul_overflow(count, s.shape[i], &count);
   bool match = false;
   if (b.shape.size() == s.shape.size() + 1)
     match = b.shape[lead] == n && b.shape[lead + 1] == kb && b.shape[lead + 2] == 16;
@@ -314,7 +326,13 @@ int mx_load_mxfp4(mx_ctx* ctx, const char* path, const char* blocks_name, const 
   for (size_t i = 0; match && i < lead; i++) match = b.shape[i] == s.shape[i];
   if (!match || n <= 0 || kb <= 0 || count <= 0)
     return mx_ctx_error(ctx, MX_EINVAL, "MXFP4 blocks and scales shapes do not match ([..., n, k/32, 16] and [..., n, k/32]).");
-  const unsigned long long data_bytes = (unsigned long long)count * n * kb * 16, scale_bytes = (unsigned long long)count * n * kb;
+  // counts are returned as int, and the byte sizes must not wrap
+  long long scale_ll = 0, data_ll = 0;
+  if (overflow || n > INT_MAX || kb > INT_MAX / 32 || count > INT_MAX ||
+      __builtin_mul_overflow(count, n, &scale_ll) || __builtin_mul_overflow(scale_ll, kb, &scale_ll) ||
+      __builtin_mul_overflow(scale_ll, 16LL, &data_ll))
+    return mx_ctx_error(ctx, MX_EINVAL, "MXFP4 tensor shape is too large.");
+  const unsigned long long data_bytes = (unsigned long long)data_ll, scale_bytes = (unsigned long long)scale_ll;
   if (b.end - b.begin != data_bytes || s.end - s.begin != scale_bytes)
     return mx_ctx_error(ctx, MX_EINVAL, "MXFP4 tensor byte sizes do not match their shapes.");
   void* d = nullptr;

@@ -95,3 +95,21 @@ def test_load_rejects_mismatched_tensors(dev, tmp_path):
     for b, s in (("a.blocks", "a.scales"), ("b.blocks", "b.scales"), ("a.blocks", "missing")):
         with pytest.raises(M.MxError):
             dev.load_mxfp4(path, b, s)
+
+
+def test_load_rejects_overflowing_shapes(dev, tmp_path):
+    """Shapes whose element or byte counts overflow, or exceed the int
+    outputs, are rejected with MX_EINVAL before anything is allocated."""
+    import json
+    import struct
+    for s_shape, b_shape in (([1 << 62, 4, 1], [1 << 62, 4, 1, 16]),     # count * n * kb wraps
+                             ([1 << 31, 1], [1 << 31, 1, 16]),           # n beyond INT_MAX
+                             ([3, 1 << 40, 2], [3, 1 << 40, 2, 16])):
+        hdr = {"b": {"dtype": "U8", "shape": b_shape, "data_offsets": [0, 16]},
+               "s": {"dtype": "U8", "shape": s_shape, "data_offsets": [16, 17]}}
+        text = json.dumps(hdr).encode()
+        p = tmp_path / "o.safetensors"
+        p.write_bytes(struct.pack("<Q", len(text)) + text + bytes(17))
+        with pytest.raises(M.MxError) as e:
+            dev.load_mxfp4(p, "b", "s")
+        assert e.value.code == M.MX_EINVAL

@@ -66,3 +66,15 @@ def test_errors(tmp_path):
         M.safetensors_find(short, "x")
     with pytest.raises(M.MxError):
         M.safetensors_find(tmp_path / "nope.safetensors", "x")
+
+
+@pytest.mark.parametrize("shape_txt", ["[99999999999999999999999]", "[-]", "[9223372036854775808]", "[1, -]"])
+def test_oversized_or_malformed_integers_fail_cleanly(tmp_path, shape_txt):
+    """The header is untrusted: an integer outside long long (or a bare minus
+    sign) is a parse error reported as a status, not an exception across the
+    C ABI."""
+    text = ('{"x": {"dtype": "U8", "shape": %s, "data_offsets": [0, 4]}}' % shape_txt).encode()
+    p = tmp_path / "big.safetensors"
+    p.write_bytes(struct.pack("<Q", len(text)) + text + bytes(4))
+    with pytest.raises(M.MxError):
+        M.safetensors_find(p, "x")
