@@ -189,6 +189,20 @@ int mx_swiglu(mx_ctx* ctx, const void* gate, const void* up, void* mid, const mx
 int mx_mlp_forward(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const void* x,
                    const mx_mlp_weights* w, void* out);
 
+/* Allocation-free forward.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels
+ * and results as mx_mlp_forward, but its scratch (mid activations, split-K
+ * partials, re-quantized operands) lives in one static device array of
+ * MX_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; it calls no
+ * hipMalloc / hipFree.  Shapes needing more scratch fail with MX_EINVAL
+ * (e.g. the decode and C0-C2 shapes fit, C4 W4A4 does not).  Every call on
+ * one GPU shares that array: calls that overlap on one GPU (two contexts or
+ * two streams at once) race; calls in one stream order are fine. */
+#define MX_NOALLOC_SCRATCH_BYTES (32u << 20)
+int mx_mlp_forward_noalloc(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const void* x,
+                           const mx_mlp_weights* w, void* out);
+
 /* Timed loop as runMXFP4FusedMLPBenchmarkVariant (main.swift:1953-2031):
  * `warmup` untimed iterations, then `iterations` back-to-back forwards on the
  * stream between two HIP events.  Iteration i uses weight set i % n_sets

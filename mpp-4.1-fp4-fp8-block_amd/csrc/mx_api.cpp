@@ -10,6 +10,7 @@
 #include <cstring>
 #include <algorithm>
 #include <functional>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -29,7 +30,19 @@ struct mx_ctx {
   hipEvent_t t0 = nullptr, t1 = nullptr;  // mx_timer_start / mx_timer_stop
 };
 
+// Scratch of mx_mlp_forward_noalloc: one static device array, which every
+// GPU the library runs on holds until the process ends.  In host code the
+// array's name is a host-side stand-in, never a device address: the address
+// comes from hipGetSymbolAddress, once per device at mx_create with that
+// device current, and only that address is handed to kernels.
+static __device__ __align__(256) uint8_t scratch[MX_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};            // device address of `scratch`, per device
+hipError_t g_scratch_err[kMaxDevices] = {};       // hipGetSymbolAddress's failure, if any
 
 int set_err(mx_ctx* c, int code, const char* fmt, ...) {
   if (c) {
@@ -173,8 +186,11 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
   return s;
 }
 
+// fixed_ws: scratch memory of fixed_ws_bytes to use instead of the
+// context's workspace (the allocation-free forward); nothing is allocated.
 int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void* x,
-                    const mx_mlp_weights* w, void* out, std::vector<Step>& steps) {
+                    const mx_mlp_weights* w, void* out, std::vector<Step>& steps, uint8_t* fixed_ws = nullptr,
+                    size_t fixed_ws_bytes = 0) {
   int rc = check_mlp_cfg(c, variant, cfg);
   if (rc) return rc;
   if (!x || !w || !out) return set_err(c, MX_EINVAL, "MLP buffers must not be null.");
@@ -188,8 +204,16 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
   if (!aligned16(x) || !aligned16(out))
     return set_err(c, MX_EINVAL, "Activation and output buffers must be 16-byte aligned.");
   MlpScratch s = plan_scratch(variant, cfg);
-  if ((rc = ensure_ws(c, s.total))) return rc;
-  uint8_t* ws = static_cast<uint8_t*>(c->ws);
+  uint8_t* ws = fixed_ws;
+  if (fixed_ws) {
+    if (s.total > fixed_ws_bytes)
+      return set_err(c, MX_EINVAL,
+                     "This MLP needs %zu bytes of scratch; the allocation-free forward has %zu (use mx_mlp_forward).",
+                     s.total, fixed_ws_bytes);
+  } else {
+    if ((rc = ensure_ws(c, s.total))) return rc;
+    ws = static_cast<uint8_t*>(c->ws);
+  }
   hipStream_t st = c->stream;
   const int T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
   const uint8_t* wg = static_cast<const uint8_t*>(w->gate.data);
@@ -319,6 +343,18 @@ int mx_create(int device, mx_ctx** out) {
   if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
     delete c;
     return MX_EGPU;
+  }
+  if (device < kMaxDevices) {  // the allocation-free forward's scratch, once per device
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+      void* p = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e == hipSuccess && p) g_scratch_ptr[device] = p;
+      else {  // reported by mx_mlp_forward_noalloc; every other entry point works without it
+        g_scratch_err[device] = e == hipSuccess ? hipErrorInvalidSymbol : e;
+        (void)hipGetLastError();
+      }
+    }
   }
   c->stream = c->own_stream;
   *out = c;
@@ -654,6 +690,25 @@ int mx_mlp_forward(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void*
   if (!c) return MX_EINVAL;
   std::vector<Step> steps;
   if (int rc = build_mlp_steps(c, variant, cfg, x, w, out, steps)) return rc;
+  return run_steps(c, steps);
+}
+
+int mx_mlp_forward_noalloc(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void* x,
+                           const mx_mlp_weights* w, void* out) {
+  if (!c) return MX_EINVAL;
+  void* p = nullptr;
+  hipError_t e = hipErrorInvalidDevice;
+  if (c->device < kMaxDevices) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[c->device];
+    e = g_scratch_err[c->device];
+  }
+  if (!p)
+    return set_err(c, MX_EGPU, "The allocation-free forward has no scratch address on device %d: %s.", c->device,
+                   hipGetErrorString(e));
+  std::vector<Step> steps;
+  if (int rc = build_mlp_steps(c, variant, cfg, x, w, out, steps, static_cast<uint8_t*>(p), MX_NOALLOC_SCRATCH_BYTES))
+    return rc;
   return run_steps(c, steps);
 }
 

@@ -27,7 +27,7 @@ EXPORTS = [
     "mx_set_stream", "mx_get_stream", "mx_sync", "mx_timer_start", "mx_timer_stop", "mx_alloc", "mx_free", "mx_upload",
     "mx_download", "mx_memset", "mx_roundtrip", "mx_pack", "mx_unpack", "mx_mxfp4_quantize",
     "mx_mxfp4_dequant_f16", "mx_mxfp4_matmul", "mx_gemm_f16", "mx_gemm_i8", "mx_accum_gemm", "mx_swiglu", "mx_mlp_forward",
-    "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_moe_forward", "mx_moe_benchmark",
+    "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_mlp_forward_noalloc", "mx_moe_forward", "mx_moe_benchmark",
     "mx_safetensors_find", "mx_load_mxfp4",
     "mx_fmt_quantize", "mx_fmt_mlp_forward",
     "mx_fmt_mlp_benchmark", "mx_fill_normal", "mx_lcg_bytes", "mx_lcg_pattern", "mx_lcg_half",
@@ -111,6 +111,7 @@ def load() -> ctypes.CDLL:
         "mx_accum_gemm": (_int, [_vp, _int, _vp, _int, _vp, _vp, _int, _int, _int, _int]),
         "mx_swiglu": (_int, [_vp, _vp, _vp, _vp, P(MlpConfig), _int]),
         "mx_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
+        "mx_mlp_forward_noalloc": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp, _int,
                                     _int, _int, P(ctypes.c_double), P(ctypes.c_double), P(_int)]),
         "mx_mlp_kernel_name": (ctypes.c_char_p, [_int, ctypes.c_void_p, _int]),
@@ -297,6 +298,13 @@ class Device:
         cfg = MlpConfig(tokens, hidden, inter)
         self._check(load().mx_mlp_forward(self.ctx, variant, ctypes.byref(cfg), x.p,
                                           ctypes.byref(w), out.p))
+
+    def mlp_forward_noalloc(self, variant, tokens, hidden, inter, x: DevBuf, w: MlpWeights, out: DevBuf):
+        """mx_mlp_forward with the library's static scratch array (no device
+        allocation)."""
+        cfg = MlpConfig(tokens, hidden, inter)
+        self._check(load().mx_mlp_forward_noalloc(self.ctx, variant, ctypes.byref(cfg), x.p,
+                                                  ctypes.byref(w), out.p))
 
     def mlp_benchmark(self, variant, tokens, hidden, inter, x: DevBuf, sets, out: DevBuf,
                       warmup=1, iterations=20, per_kernel=True, graph=True):
