@@ -70,10 +70,12 @@ def make_sets(dev, M, T, H, I, n_sets, seed, wfmt=0):
     return x, sets, bufs
 
 
-def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt=0):
+def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt=0, cpu=None):
     """Time `iters` forwards twice: replayed from one HIP graph (the value;
     the reference likewise pre-encodes all iterations in one command buffer)
-    and launched one by one on the stream (reported as stream_us_per_iter)."""
+    and launched one by one on the stream (reported as stream_us_per_iter).
+    cpu: None, or the token count of the CPU baseline sample run on this
+    row's own inputs (weight set 0) before they are freed."""
     x, sets, bufs = make_sets(dev, M, T, H, I, n_sets, seed, wfmt)
     out = dev.alloc(T * H * 4)
     if wfmt:
@@ -93,6 +95,8 @@ def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt
            "us_per_iter": round(us, 3), "tflops": round(flops / (us * 1e-6) / 1e12, 3),
            "stream_us_per_iter": round(ssecs / iters * 1e6, 3),
            "kernel_us": {k: round(v, 3) for k, v in kern.items()}}
+    if cpu:
+        res["cpu_baseline"] = cpu_row(dev, M, variant, wfmt, T, H, I, x, bufs[:6], out, cpu)
     for b in bufs + [x, out]:
         b.free()
     log(f"[bench] {name}: {us:.2f} us/iter (stream {res['stream_us_per_iter']}), "
@@ -133,32 +137,72 @@ def run_moe(dev, M, name, E, per_expert, H, I, iters, warmup, seed):
     return res
 
 
-def cpu_baseline(T, H, I, budget_s=12.0):
-    """Time the CPU oracle's MLP (f16 activations, MXFP4 weights) on host
-    cores, on the same shapes with data generated on the host."""
+CPU_THREADS = 16  # the GPU box's CPU share for one GPU (its nproc may show more)
+
+
+def cpu_row(dev, M, variant, wfmt, T, H, I, x, wbufs, out, tokens, budget_s=12.0):
+    """The CPU baseline of one configuration, on that GPU row's own inputs:
+    x and weight set 0 are downloaded, and the CPU port (oracle/mx_oracle.c,
+    the reference's one-output-per-dot-product loop restated,
+    PackedNumericKernels.metal:542-581 and 801-832, with BASELINE's
+    dequantize-then-FP32-accumulate semantics) runs the first `tokens`
+    tokens on CPU_THREADS host threads.  A sample smaller than T is scaled
+    to the whole job and labelled extrapolated.  Its output is checked
+    against the GPU's for the same tokens (max-abs / rms, cosine)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    threads = min(16, os.cpu_count() or 1)
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal((T, H)).astype(np.float16)
-    qs = []
-    for n, k in ((I, H), (I, H), (H, I)):
-        w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
-        qs += list(O.mxfp4_quantize(w))
-    O.mlp_mxfp4(O.MLP_F16, x, *qs, H, I, threads=threads)      # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.mlp_mxfp4(O.MLP_F16, x, *qs, H, I, threads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 100000:
-            break
-    us = el / n * 1e6
+    threads = min(CPU_THREADS, os.cpu_count() or 1)
+    xh = dev.download(x, np.float16, (T, H))[:tokens].copy()
+    mats = []
+    for j, (n, k) in enumerate(((I, H), (I, H), (H, I))):
+        q, sc = wbufs[2 * j], wbufs[2 * j + 1]
+        if not wfmt:
+            mats += [dev.download(q, np.uint8, (n, k // 2)), dev.download(sc, np.uint8, (n, k // 32))]
+        elif wfmt == M.WFMT_INT4:
+            mats += [dev.download(q, np.uint8, (n, k // 2)), dev.download(sc, np.float16, (n, k // 32))]
+        else:
+            mats += [dev.download(q, np.uint8, (n, k)), dev.download(sc, np.float32, (n,))]
+    w0 = M.Device.weights(*[(wbufs[2 * j], wbufs[2 * j + 1]) for j in range(3)])
+    if wfmt:
+        dev.fmt_mlp_forward(wfmt, T, H, I, x, w0, out)
+        mode = None
+    else:
+        dev.mlp_forward(variant, T, H, I, x, w0, out)
+        mode = {M.MLP_FUSED: O.MLP_F16, M.MLP_DEQUANT: O.MLP_F16, M.MLP_W4A4: O.MLP_W4A4}[variant]
+    gpu = dev.download(out, np.float16, (T, H))[:tokens]
+
+    def run():
+        if wfmt:
+            return O.mlp_format(wfmt, xh, *mats, H, I, threads=threads)
+        return O.mlp_mxfp4(mode, xh, *mats, H, I, threads=threads)
+
+    O.set_accum_f32(True)
+    try:
+        flops = 6.0 * tokens * H * I
+        if flops < 5e9:
+            run()  # one warm run where it is cheap
+        n, t0 = 0, time.perf_counter()
+        while True:
+            ref = run()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or flops * (n + 1) > 1e11:
+                break
+    finally:
+        O.set_accum_f32(False)
+    us = el / n * 1e6 * (T / tokens)
+    rel, cos = O.mlp_error(gpu, ref)
+    fmt = {0: "MXFP4", 1: "FP8 E4M3", 2: "FP8 E5M2", 3: "INT8", 4: "INT4 g32", 5: "W8A8"}[wfmt]
+    what = f"{n} MLP forward(s) of {tokens} tokens" + (f", scaled x{T // tokens} (extrapolated)"
+                                                        if tokens < T else "")
     return {"value": round(6.0 * T * H * I / (us * 1e-6) / 1e12, 6), "unit": "TFLOP/s",
             "us_per_iter": round(us, 1), "cores": threads, "kind": "port",
-            "sample": f"{n} full MLP forwards at T={T} H={H} I={I} (oracle/mx_oracle.c, "
-                      f"float64 accumulation, {threads} threads), ~{el:.0f} s"}
+            "extrapolated": tokens < T,
+            "gpu_vs_cpu": {"max_abs_over_rms": round(float(rel), 6), "cosine": round(float(cos), 7)},
+            "sample": f"{what} at T={T} H={H} I={I}, {fmt} weights: this GPU row's own x and "
+                      f"weight set 0, oracle/mx_oracle.c with float32 accumulation in K order, "
+                      f"{threads} threads, {el:.1f} s"}
 
 
 def copy_probe(nbytes=256 << 20, reps=3):
@@ -224,7 +268,7 @@ def main():
     # ---- headline: config 1, T=1 ------------------------------------------
     T, H, I = 1, 7168, 2048
     prim, _ = run_config(dev, M, "C1 T=1 fused", M.MLP_FUSED, T, H, I, 24, args.steps,
-                         args.warmup, seed=1)
+                         args.warmup, seed=1, cpu=None if args.no_cpu else T)
     us = prim["us_per_iter"]
     # algorithmic bytes per launch of each kernel the decode MLP may run:
     # weights + E8M0 scales + activations in + results out (for the whole
@@ -257,26 +301,30 @@ def main():
 
     if not args.no_secondary:
         sec = {}
+        cpu = not args.no_cpu
         only = set(t for t in args.only.split(",") if t)
         want = lambda tag, variant="": not only or tag in only or f"{tag}_{variant}" in only
         if want("c1_t8"):
-            r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2)
+            r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2, cpu=cpu and 8)
             b = 3 * mxfp4_bytes(2048, 7168) + 2 * 8 * 7168 * 2
             r["hbm_frac"] = round(b / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
             sec["c1_t8_fused"] = r
         if want("c4"):
-            r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, 1, 10, 2, seed=4)
+            r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, 1, 10, 2, seed=4,
+                              cpu=cpu and 64)
             r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
             sec["c4_w4a4"] = r
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_W4A4, "w4a4")):
             if not want("c0", tag):
                 continue
-            r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, 24, 100, 10, seed=5)
+            r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, 24, 100, 10, seed=5,
+                              cpu=cpu and tag == "fused" and 128)
             sec[f"c0_{tag}"] = r
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant")):
             if not want("c2", tag):
                 continue
-            r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, 24, 100, 10, seed=6)
+            r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, 24, 100, 10, seed=6,
+                              cpu=cpu and tag == "fused" and 512)
             r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
             sec[f"c2_{tag}"] = r
         for wfmt, tag in ((M.WFMT_FP8_E4M3, "fp8_e4m3"), (M.WFMT_FP8_E5M2, "fp8_e5m2"),
@@ -284,7 +332,7 @@ def main():
             if not want("c3", tag):
                 continue
             r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, 2, 40, 4, seed=7,
-                              wfmt=wfmt)
+                              wfmt=wfmt, cpu=cpu and 128)
             wb = 3 * 4096 * 14336 * (0.5 if wfmt == M.WFMT_INT4 else 1)
             r["hbm_frac"] = round(wb / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
             sec[f"c3_{tag}"] = r
@@ -299,7 +347,7 @@ def main():
         result["secondary"] = sec
 
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(T, H, I)
+        result["cpu_baseline"] = prim.pop("cpu_baseline")
     dev.close()
     print(json.dumps(result), flush=True)
 

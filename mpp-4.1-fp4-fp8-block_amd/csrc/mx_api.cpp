@@ -153,8 +153,8 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
   if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
     s.mid = take(T * I * 2);
     const int e = variant == MX_MLP_REFROW ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16;
-    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, e, (int)T, (int)I, (int)H),
-                          mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_STORE_F32, (int)T, (int)H, (int)I)));
+    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_MXFP4, e, (int)T, (int)I, (int)H),
+                          mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_MXFP4, mx::EPI_STORE_F32, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_DEQUANT) {
     s.wg = take(I * H * 2);
     s.wu = take(I * H * 2);
@@ -162,8 +162,8 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
     s.gate = take(T * I * 4);
     s.up = take(T * I * 4);
     s.mid = take(T * I * 4);
-    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_STORE_F32, (int)T, (int)I, (int)H),
-                          mx::gemm_q_ws_bytes(mx::AK_F32, mx::EPI_STORE_F16, (int)T, (int)H, (int)I)));
+    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, (int)T, (int)I, (int)H),
+                          mx::gemm_q_ws_bytes(mx::AK_F32, mx::BK_F16, mx::EPI_STORE_F16, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_W4A4) {
     s.xq = take(T * H / 2);
     s.mq = take(T * I / 2);
@@ -548,7 +548,7 @@ static int run_gemm(mx_ctx* c, const void* a, int a_dtype, int bk, const void* b
                     void* out, int epi, int m, int n, int k, size_t ws_off = 0) {
   const int ak = a_dtype == MX_DTYPE_F32 ? mx::AK_F32 : mx::AK_F16;
   if (mx::gemm_q_ok(ak, bk, epi, m, n, k)) {
-    const size_t wsb = mx::gemm_q_ws_bytes(ak, epi, m, n, k);
+    const size_t wsb = mx::gemm_q_ws_bytes(ak, bk, epi, m, n, k);
     if (int rc = ensure_ws(c, ws_off + wsb)) return rc;
     void* part = wsb ? static_cast<uint8_t*>(c->ws) + ws_off : nullptr;
     mx::QGemmArgs g{a, nullptr, b, scales, nullptr, nullptr, out, part, m, n, k, 0};
@@ -586,7 +586,7 @@ int mx_gemm_i8(mx_ctx* c, const int8_t* a, const int8_t* b, int32_t* out, int m,
   if (int rc = check_gemm(c, m, n, k, a, b, out)) return rc;
   if (!mx::gemm_q_ok(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_I32, m, n, k))
     return set_err(c, MX_EINVAL, "int8 matmul needs n %% 64 == 0 and k %% 128 == 0.");
-  const size_t wsb = mx::gemm_q_ws_bytes(mx::AK_I8, mx::EPI_STORE_I32, m, n, k);
+  const size_t wsb = mx::gemm_q_ws_bytes(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_I32, m, n, k);
   if (int rc = ensure_ws(c, wsb)) return rc;
   mx::QGemmArgs g{a, nullptr, b, nullptr, nullptr, nullptr, out, wsb ? c->ws : nullptr, m, n, k, 0};
   MX_HIP(c, mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_I32, g, c->stream));
@@ -630,7 +630,7 @@ int mx_accum_gemm(mx_ctx* c, int a_fmt, const void* a, int b_fmt, const void* b,
   const size_t plane = hq ? align_up((size_t)n * (kp / 32), 256) : h4 ? align_up((size_t)n * (kp / 32) * 2, 256) : 0;
   const int ak = i44 ? mx::AK_I8 : mx::AK_F16;
   const int bk = hq ? mx::BK_MXFP4 : h4 ? mx::BK_INT4G32 : i44 ? mx::BK_I8 : mx::BK_F16;
-  const size_t part = !qq && mx::gemm_q_ok(ak, bk, epi, m, n, (int)kp) ? mx::gemm_q_ws_bytes(ak, epi, m, n, (int)kp) : 0;
+  const size_t part = !qq && mx::gemm_q_ok(ak, bk, epi, m, n, (int)kp) ? mx::gemm_q_ws_bytes(ak, bk, epi, m, n, (int)kp) : 0;
   if (int rc = ensure_ws(c, a_sz + b_sz + plane + part)) return rc;
   uint8_t* ws = static_cast<uint8_t*>(c->ws);
   const uint8_t* ua = static_cast<const uint8_t*>(a);
@@ -964,8 +964,8 @@ static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const 
     auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
     const size_t o_xq = take((size_t)T * H), o_xs = take((size_t)T * 4), o_mid = take((size_t)T * I * 4),
                  o_mq = take((size_t)T * I), o_ms = take((size_t)T * 4),
-                 o_qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_I8, mx::EPI_SWIGLU_F32, T, I, H),
-                                       mx::gemm_q_ws_bytes(mx::AK_I8, mx::EPI_STORE_F16, T, H, I)));
+                 o_qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_I8, mx::BK_I8, mx::EPI_SWIGLU_F32, T, I, H),
+                                       mx::gemm_q_ws_bytes(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_F16, T, H, I)));
     if (int rc = ensure_ws(c, off)) return rc;
     uint8_t* ws = static_cast<uint8_t*>(c->ws);
     int8_t* xq = reinterpret_cast<int8_t*>(ws + o_xq);
@@ -983,8 +983,8 @@ static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const 
     return MX_OK;
   }
   const size_t mid_b = align_up((size_t)T * I * 2, 256);
-  const size_t qws_b = std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_SWIGLU_F16, T, I, H),
-                                mx::gemm_q_ws_bytes(mx::AK_F16, mx::EPI_STORE_F16, T, H, I));
+  const size_t qws_b = std::max(mx::gemm_q_ws_bytes(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, T, I, H),
+                                mx::gemm_q_ws_bytes(mx::AK_F16, bk, mx::EPI_STORE_F16, T, H, I));
   if (int rc = ensure_ws(c, mid_b + qws_b)) return rc;
   uint16_t* mid = static_cast<uint16_t*>(c->ws);
   void* qws = static_cast<uint8_t*>(c->ws) + mid_b;

@@ -79,6 +79,8 @@ __device__ __forceinline__ void dma16(const void* src, void* lds) {
 
 // s_waitcnt immediate (gfx9 encoding): vmcnt(n) only.
 constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// s_waitcnt lgkmcnt(0) alone (vmcnt 63, expcnt 7).
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
 
 // INT8 x8 -> f16 x8 (exact): byte b -> half(1024 + (b ^ 0x80)) - 1152.
 __device__ __forceinline__ v8h i8x8_to_f16(uint32_t w0, uint32_t w1) {
@@ -180,8 +182,13 @@ constexpr int out_bytes(int epi) {
 // 64-K stage and an 8-bit one 64; B is staged BCH stages at a time (4 and 2)
 // so that every DMA moves whole 128-byte lines (8 rows per instruction), the
 // fastest LDS-DMA pattern.  BCH = 1 stages B per stage.
-template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH>
-__global__ __launch_bounds__(256, 2) void k_gemm_q(
+// NS: LDS slots of the per-stage ring.  2 (default): one stage in flight
+// while one is computed, small enough for two workgroups per CU.  4: three
+// stages in flight, for launches of at most one workgroup per CU, which
+// otherwise sit in the DMA latency of every stage (8-bit / f16 weights,
+// BCH = 1 only).
+template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2>
+__global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
   constexpr bool DUAL = is_dual(EPI);
   if constexpr (GROUPED) {
@@ -211,12 +218,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
   constexpr int KSTEPS = 4;
   static_assert(NA >= 1 && (NBC >= 4 ? NBC % 4 == 0 : true), "tile / stage mismatch");
   static_assert(BCH == 1 || RBC == 128, "B chunks are whole 128-byte lines");
+  static_assert(NS == 2 || (NS == 4 && BCH == 1 && !SCALES4 && !GROUPED), "deep ring: per-stage B, no scales");
   using AccT = typename std::conditional<AK == AK_I8, v16i, v16f>::type;
 
-  __shared__ __attribute__((aligned(16))) uint8_t a_s0[kTM * RA];
-  __shared__ __attribute__((aligned(16))) uint8_t a_s1[kTM * RA];
-  __shared__ __attribute__((aligned(16))) uint8_t b_s0[TBR * RBC];
-  __shared__ __attribute__((aligned(16))) uint8_t b_s1[TBR * RBC];
+  // One __shared__ array per slot: the compiler then knows that a DMA into
+  // one slot does not write what the fragment reads of another slot read.
+  // (Its wait insertion tells at most eight DMA targets apart, so the deep
+  // ring keeps A and B of a slot in one array: four targets.)
+  constexpr int SA = NS == 2 ? kTM * RA : 16, SB = NS == 2 ? TBR * RBC : 16;
+  constexpr int SD = NS > 2 ? kTM * RA + TBR * RBC : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t a_s0[SA];
+  __shared__ __attribute__((aligned(16))) uint8_t a_s1[SA];
+  __shared__ __attribute__((aligned(16))) uint8_t b_s0[SB];
+  __shared__ __attribute__((aligned(16))) uint8_t b_s1[SB];
+  __shared__ __attribute__((aligned(16))) uint8_t d_s0[SD];
+  __shared__ __attribute__((aligned(16))) uint8_t d_s1[SD];
+  __shared__ __attribute__((aligned(16))) uint8_t d_s2[SD];
+  __shared__ __attribute__((aligned(16))) uint8_t d_s3[SD];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -316,31 +334,52 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
   // loads one wave issues per stage (A + scales); a B chunk adds NB
   constexpr int VM_A = NA + (SCALES4 ? NWB : 0);
 
-#define MXQ_COMPUTE(AS, BS, P, POS)                                                                   \
+  // One stage's MFMAs, in two halves.  MXQ_READ issues every LDS fragment
+  // read of the stage into registers (AR, BR); MXQ_MATH widens the weights
+  // and runs the MFMAs from them.  Reading the whole stage first exposes one
+  // LDS latency per stage instead of one per k-step (left to itself the
+  // compiler reuses one register set and waits lgkmcnt(0) before each
+  // k-step), and the deep ring reads stage st+1 while stage st's MFMAs run.
+  //   AR[s][i][w]  A block i, k-step s: 16 bytes (f16 / int8) or 2 x 16 (f32)
+  //   BR[u][j]     B block j: one 16-byte read per k-step (f16 / int8),
+  //                per 2 k-steps (8-bit), per stage (4-bit)
+  //   CO           the stage's first 16-byte chunk within a B row (chunked B)
+  constexpr int BREADS = (BK == BK_MXFP4 || BK == BK_INT4G32) ? 1 : (AK != AK_I8 && BK != BK_F16) ? 2 : KSTEPS;
+  constexpr int AW = AK == AK_F32 ? 2 : 1;
+#define MXQ_READ(AS, BS, CO, AR, BR)                                                               \
   {                                                                                                \
     _Pragma("unroll") for (int s = 0; s < KSTEPS; s++) {                                           \
-      if (AK == AK_I8) {                                                                           \
-        v4i af[2], bf[NWB];                                                                         \
-        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                            \
-          const int r_ = wm * 64 + i * 32 + r32;                                                   \
-          af[i] = *reinterpret_cast<const v4i*>((AS) + r_ * RA + (((4 * h + s) ^ swz<RA>(r_)) << 4)); \
+      _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
+        const int r_ = wm * 64 + i * 32 + r32;                                                     \
+        _Pragma("unroll") for (int w = 0; w < AW; w++) {                                           \
+          const int ch_ = AK == AK_F32 ? 8 * h + 2 * s + w : 4 * h + s;                            \
+          AR[s][i][w] = *reinterpret_cast<const v4i*>((AS) + r_ * RA + ((ch_ ^ swz<RA>(r_)) << 4)); \
         }                                                                                          \
-        _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                           \
-          const int r_ = b_blk[j] + r32;                                                           \
-          bf[j] = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + 4 * h + s) ^ swz<RBC>(r_)) << 4)); \
-        }                                                                                          \
+      }                                                                                            \
+    }                                                                                              \
+    _Pragma("unroll") for (int u = 0; u < BREADS; u++) {                                           \
+      _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                            \
+        const int r_ = b_blk[j] + r32;                                                             \
+        const int ch_ = (CO) + (BREADS == 1 ? h : BREADS == 2 ? 2 * h + u : 4 * h + u);            \
+        BR[u][j] = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((ch_ ^ swz<RBC>(r_)) << 4));  \
+      }                                                                                            \
+    }                                                                                              \
+  }
+#define MXQ_MATH(AR, BR, P)                                                                        \
+  {                                                                                                \
+    _Pragma("unroll") for (int s = 0; s < KSTEPS; s++) {                                           \
+      if constexpr (AK == AK_I8) {                                                                 \
         _Pragma("unroll") for (int i = 0; i < 2; i++)                                              \
           _Pragma("unroll") for (int j = 0; j < NWB; j++)                                           \
-            acc[i][j] = (AccT)__builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], (v16i)acc[i][j], 0, 0, 0); \
+            acc[i][j] = (AccT)__builtin_amdgcn_mfma_i32_32x32x32_i8(AR[s][i][0], BR[s][j], (v16i)acc[i][j], 0, 0, 0); \
       } else {                                                                                     \
-        v8h af[2], bf[NWB];                                                                         \
+        v8h af[2], bf[NWB];                                                                        \
         _Pragma("unroll") for (int i = 0; i < 2; i++) {                                            \
-          const int r_ = wm * 64 + i * 32 + r32;                                                   \
-          if (AK == AK_F16) {                                                                      \
-            af[i] = *reinterpret_cast<const v8h*>((AS) + r_ * RA + (((4 * h + s) ^ swz<RA>(r_)) << 4)); \
+          if constexpr (AK == AK_F16) {                                                            \
+            af[i] = __builtin_bit_cast(v8h, AR[s][i][0]);                                          \
           } else {                                                                                 \
-            const v4f lo_ = *reinterpret_cast<const v4f*>((AS) + r_ * RA + (((8 * h + 2 * s) ^ swz<RA>(r_)) << 4)); \
-            const v4f hi_ = *reinterpret_cast<const v4f*>((AS) + r_ * RA + (((8 * h + 2 * s + 1) ^ swz<RA>(r_)) << 4)); \
+            const v4f lo_ = __builtin_bit_cast(v4f, AR[s][i][0]);                                  \
+            const v4f hi_ = __builtin_bit_cast(v4f, AR[s][i][AW - 1]);                             \
             _Pragma("unroll") for (int t = 0; t < 4; t++) {                                        \
               af[i][t] = (_Float16)lo_[t];                                                         \
               af[i][4 + t] = (_Float16)hi_[t];                                                     \
@@ -348,15 +387,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
           }                                                                                        \
         }                                                                                          \
         _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                           \
-          const int r_ = b_blk[j] + r32;                                                           \
-          if (BK == BK_F16) {                                                                      \
-            bf[j] = *reinterpret_cast<const v8h*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + 4 * h + s) ^ swz<RBC>(r_)) << 4)); \
-          } else if (BK == BK_MXFP4 || BK == BK_INT4G32) {                                         \
-            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + h) ^ swz<RBC>(r_)) << 4)); \
+          if constexpr (BK == BK_F16) {                                                            \
+            bf[j] = __builtin_bit_cast(v8h, BR[s][j]);                                             \
+          } else if constexpr (BK == BK_MXFP4 || BK == BK_INT4G32) {                               \
+            const v4i w_ = BR[0][j];                                                               \
             if (BK == BK_MXFP4) bf[j] = fp4x8_dequant_f16(w_[s], scv[P][j]);                       \
             else bf[j] = i4x8_to_f16(w_[s], __builtin_bit_cast(_Float16, (uint16_t)scv[P][j]));    \
           } else {                                                                                 \
-            const v4i w_ = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((((POS) * (RB / 16) + 2 * h + (s >> 1)) ^ swz<RBC>(r_)) << 4)); \
+            const v4i w_ = BR[s >> 1][j];                                                          \
             const uint32_t w0_ = (s & 1) ? w_[2] : w_[0], w1_ = (s & 1) ? w_[3] : w_[1];          \
             if (BK == BK_INT8) bf[j] = i8x8_to_f16(w0_, w1_);                                      \
             else bf[j] = fp8x8_to_f16<BK>(w0_, w1_);                                               \
@@ -367,6 +405,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
             acc[i][j] = (AccT)mfma_f16_32x32x16(af[i], bf[j], (v16f)acc[i][j]);                    \
       }                                                                                            \
     }                                                                                              \
+  }
+  // The 2-slot loops: a stage's reads, then its math, then every read of the
+  // slot has landed before the barrier that frees it.  POS: the stage's
+  // place within its B chunk (B rows hold BCH stages).
+#define MXQ_COMPUTE(AS, BS, P, POS)                                                                \
+  {                                                                                                \
+    v4i ar_[KSTEPS][2][AW];                                                                        \
+    v4i br_[BREADS][NWB];                                                                          \
+    MXQ_READ(AS, BS, (POS) * (RB / 16), ar_, br_)                                                  \
+    __builtin_amdgcn_sched_barrier(0); /* keep the reads ahead of the MFMAs */                     \
+    MXQ_MATH(ar_, br_, P)                                                                          \
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);                                                        \
   }
 
   // Pipeline, one B stage per A stage (BCH = 1): stage k+1's DMA is in
@@ -404,6 +454,51 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
       __builtin_amdgcn_s_barrier();                                                                \
     }                                                                                              \
   }
+  // Deep ring (NS = 4, KT % 4 == 0, KT >= 8): stage st sits in slot st % 4
+  // and four stages are in flight from the start; the LDS fragments of stage
+  // st+1 are read while stage st's MFMAs run (register sets 0 / 1 by
+  // parity).  Iteration st:
+  //   1. wait until stage st's fragments are in registers (lgkmcnt) and
+  //      stage st+1's DMA has landed (vmcnt retires in issue order: only
+  //      stages st+2, st+3 may remain), then one barrier.  Past it every
+  //      wave has finished reading slot st, and stage st+1 is complete.
+  //   2. refill slot st with stage st+4 (past the end: stage KT-1 again, so
+  //      the wait count stays constant; those copies are never read).
+  //   3. read stage st+1's fragments (after the last stage: a slot holding
+  //      a repeated copy, never used), then stage st's MFMAs.
+#define MXQ_AS(i) ((i) == 0 ? d_s0 : (i) == 1 ? d_s1 : (i) == 2 ? d_s2 : d_s3)
+#define MXQ_BS(i) (MXQ_AS(i) + kTM * RA)
+#define MXQ_DEEP(U, CUR, NXT)                                                                      \
+  {                                                                                                \
+    const int st_ = kt + (U);                                                                      \
+    if (b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm((NS - 2) * (VM_A + NB)) & ~(15 << 8));        \
+    else __builtin_amdgcn_s_waitcnt(wait_vm((NS - 2) * VM_A) & ~(15 << 8));                        \
+    __builtin_amdgcn_s_barrier();                                                                  \
+    __builtin_amdgcn_sched_barrier(0);                                                             \
+    MXQ_DMA_A(min(st_ + NS, KT - 1), MXQ_AS(U))                                                    \
+    MXQ_DMA_B(min(st_ + NS, KT - 1), MXQ_BS(U))                                                    \
+    MXQ_READ(MXQ_AS(((U) + 1) % NS), MXQ_BS(((U) + 1) % NS), 0, NXT##_a, NXT##_b)                  \
+    __builtin_amdgcn_sched_barrier(0);                                                             \
+    MXQ_MATH(CUR##_a, CUR##_b, 0)                                                                  \
+  }
+  if constexpr (NS > 2) {
+    static_assert(NS == 4 && (NS - 1) * (VM_A + NB) <= 63, "vmcnt range");
+    v4i f0_a[KSTEPS][2][AW], f1_a[KSTEPS][2][AW];
+    v4i f0_b[BREADS][NWB], f1_b[BREADS][NWB];
+    MXQ_DMA_A(0, MXQ_AS(0)) MXQ_DMA_B(0, MXQ_BS(0))
+    MXQ_DMA_A(1, MXQ_AS(1)) MXQ_DMA_B(1, MXQ_BS(1))
+    MXQ_DMA_A(2, MXQ_AS(2)) MXQ_DMA_B(2, MXQ_BS(2))
+    MXQ_DMA_A(3, MXQ_AS(3)) MXQ_DMA_B(3, MXQ_BS(3))
+    if (b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm((NS - 1) * (VM_A + NB)));
+    else __builtin_amdgcn_s_waitcnt(wait_vm((NS - 1) * VM_A));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    MXQ_READ(MXQ_AS(0), MXQ_BS(0), 0, f0_a, f0_b)
+    __builtin_amdgcn_sched_barrier(0);
+    for (int kt = 0; kt < KT; kt += NS) {
+      MXQ_DEEP(0, f0, f1) MXQ_DEEP(1, f1, f0) MXQ_DEEP(2, f0, f1) MXQ_DEEP(3, f1, f0)
+    }
+  } else {
   MXQ_ISSUE(0, a_s0, b_s0, 0)
   if constexpr (BCH == 1) {
     int kt = 0;
@@ -428,6 +523,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
       MXQ_BODY(4) MXQ_BODY(5) MXQ_BODY(6) MXQ_BODY(7)
     }
   }
+  }
+#undef MXQ_DEEP
+#undef MXQ_AS
+#undef MXQ_BS
 #undef MXQ_BODY
 #undef MXQ_SYNC_POINT
 #undef MXQ_ISSUE
@@ -440,6 +539,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
   // ---- epilogue, or the raw partial tile when K is split (separate loops
   // behind one uniform branch).
   constexpr int PL = DUAL ? 2 : 1;
+  // A tile whose rows are all below M stores without per-row guards: behind
+  // the guards each store sits in its own branch and the compiler waits for
+  // the previous store before reusing its address registers, one round trip
+  // per element.
+  const bool full_tile = m0 + kTM <= M;
   if (gridDim.y > 1) {
     const size_t plane = (size_t)M * g.n;
     uint32_t* w = reinterpret_cast<uint32_t*>(g.ws) + (size_t)blockIdx.y * PL * plane;
@@ -457,19 +561,40 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
           gv[v] = __builtin_bit_cast(uint32_t, ge);
           uv[v] = DUAL ? __builtin_bit_cast(uint32_t, ue) : 0u;
         }
+        auto put = [&](auto guarded) {
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, v);
-          if (row < M) {
-            const size_t o = (size_t)row * g.n + col;
-            w[o] = gv[v];
-            if (DUAL) w[plane + o] = uv[v];
+          for (int v = 0; v < 16; v++) {
+            const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, v);
+            if (!decltype(guarded)::value || row < M) {
+              const size_t o = (size_t)row * g.n + col;
+              w[o] = gv[v];
+              if (DUAL) w[plane + o] = uv[v];
+            }
           }
-        }
+        };
+        if (full_tile) put(std::false_type{});
+        else put(std::true_type{});
       }
     }
     return;
   }
+  // The scales are loaded up front, unconditionally (rows clamped), so the
+  // per-element stores below wait on none of them: left inside the row
+  // guards, each element re-loads its scales and waits for them in turn.
+  float rs[2][16];  // per-token scale of each accumulator row (W8A8)
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int v = 0; v < 16; v++)
+      rs[i][v] = AK == AK_I8 ? g.a_scale[min(m0 + wm * 64 + i * 32 + acc32_row(lane, v), M - 1)] : 1.0f;
+  float cs0[NWB], cs1 = 1.0f;  // per weight row scales (gate / single, up)
+#pragma unroll
+  for (int jj = 0; jj < NWB; jj++) {
+    const int col = DUAL ? n0 + wn * 32 + r32 : n0 + b_blk[jj] + r32;
+    cs0[jj] = row_scaled(BK) ? reinterpret_cast<const float*>(g.s0)[col] : 1.0f;
+  }
+  if (DUAL && row_scaled(BK)) cs1 = reinterpret_cast<const float*>(g.s1)[n0 + wn * 32 + r32];
+  auto epilogue = [&](auto guarded) {
 #pragma unroll
   for (int i = 0; i < 2; i++) {
 #pragma unroll
@@ -478,23 +603,31 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q(
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, v);
-        if (row >= M) continue;
+        if (decltype(guarded)::value && row >= M) continue;
         const size_t o = (size_t)row * g.n + col;
         if (EPI == EPI_STORE_I32) {
           reinterpret_cast<int*>(g.c)[o] = (int)acc[i][jj][v];
           continue;
         }
+        // same products, in the same order, as scaled(): acc * row scale * column scale
         const float g0 = AK == AK_I8 ? (float)(int)acc[i][jj][v] : (float)acc[i][jj][v];
-        const float x0 = scaled<AK, BK>(g0, g, reinterpret_cast<const float*>(g.s0), row, col);
+        float x0 = g0;
+        if (AK == AK_I8) x0 = x0 * rs[i][v];
+        if (row_scaled(BK)) x0 = x0 * cs0[jj];
         float u = 0.0f;
         if (DUAL) {
           const float u0 = AK == AK_I8 ? (float)(int)acc[i][NWB - 1][v] : (float)acc[i][NWB - 1][v];
-          u = scaled<AK, BK>(u0, g, reinterpret_cast<const float*>(g.s1), row, col);
+          u = u0;
+          if (AK == AK_I8) u = u * rs[i][v];
+          if (row_scaled(BK)) u = u * cs1;
         }
         epi_store<EPI>(g.c, o, x0, u);
       }
     }
   }
+  };
+  if (full_tile) epilogue(std::false_type{});
+  else epilogue(std::true_type{});
 }
 
 // Split-K reduction + epilogue: four consecutive output elements per thread
@@ -556,6 +689,17 @@ template <int AK, int BK> constexpr int b_chunk() {
   return (BK == BK_MXFP4 || BK == BK_INT4G32) ? 128 / b_row_bytes<BK>(AInfo<AK>::KS) : 1;
 }
 
+// Launches of at most this many workgroups (one per CU) take the deep ring,
+// for weight formats staged per stage whose four slots fit the 160 KB of LDS
+// (not f32 activations x f16 weights: 4 x 48 KB).
+constexpr int kDeepMaxWgs = 256;
+constexpr bool deep_format(int ak, int bk) {
+  const int ks = ak == AK_I8 ? 128 : 64;
+  const int ra = ak == AK_F32 ? 256 : 128;
+  const int rb = bk == BK_F16 ? ks * 2 : ks;
+  return bk != BK_MXFP4 && bk != BK_INT4G32 && 4 * 128 * (ra + rb) <= 160 * 1024;
+}
+
 template <int AK, int BK, int EPI, int NWB>
 hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   QGemmArgs g = g0;
@@ -567,6 +711,18 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   // keeps the host and device kernel-argument layouts identical)
   // chunked B once a split spans at least four chunks (a shorter split would
   // wait for its whole B up front)
+  if constexpr (deep_format(AK, BK)) {
+    if (g.tiles_m * tiles_n * splits <= kDeepMaxWgs && kt >= 8 && kt % 4 == 0) {
+      hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 4>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0,
+                         st, g, 0);
+      if (splits > 1) {
+        const size_t n = (size_t)g.m * g.n;
+        hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st, g,
+                           splits);
+      }
+      return hipGetLastError();
+    }
+  }
   if (BC > 1 && kt % BC == 0 && kt >= 4 * BC)
     hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
   else
@@ -614,17 +770,24 @@ using namespace qgemm;
 // tiles on (three quarters of the CUs busy without a split) K is not split:
 // the f32 partials would move more bytes than the weights (W8A8 at M=128,
 // N=2x14336, K=4096: 80 -> 72 us for the MLP without the split).
-int gemm_q_splits(int ak, int epi, int m, int n, int k) {
+// Formats that take the deep ring split only as far as one workgroup per
+// CU (at most 256 workgroups), keeping a multiple of 4 stages per split.
+int gemm_q_splits(int ak, int bk, int epi, int m, int n, int k) {
   const int tiles = ((m + kTM - 1) / kTM) * (is_dual(epi) ? n / 64 : (n % 128 == 0 ? n / 128 : n / 64));
   const int kt = k / stage_k(ak);
   if (tiles >= 192) return 1;
   int s = 1;
+  if (deep_format(ak, bk) && kt % 4 == 0) {
+    while (tiles * 2 * s <= kDeepMaxWgs && kt % (8 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
+    if (tiles * s >= 192) return s;  // else too few workgroups: the 2-slot policy below
+    s = 1;
+  }
   while (tiles * s < 384 && kt % (2 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
   return s;
 }
 
-size_t gemm_q_ws_bytes(int ak, int epi, int m, int n, int k) {
-  const int s = gemm_q_splits(ak, epi, m, n, k);
+size_t gemm_q_ws_bytes(int ak, int bk, int epi, int m, int n, int k) {
+  const int s = gemm_q_splits(ak, bk, epi, m, n, k);
   return s > 1 ? (size_t)s * (is_dual(epi) ? 2 : 1) * m * n * 4 : 0;
 }
 
@@ -659,7 +822,7 @@ hipError_t launch_gemm_q_grouped(int epi, const QGemmArgs& g, const GroupTable& 
 
 hipError_t launch_gemm_q(int ak, int bk, int epi, const QGemmArgs& g, hipStream_t st) {
   if (!gemm_q_ok(ak, bk, epi, g.m, g.n, g.k)) return hipErrorInvalidValue;
-  const int s = gemm_q_splits(ak, epi, g.m, g.n, g.k);
+  const int s = gemm_q_splits(ak, bk, epi, g.m, g.n, g.k);
   if (s > 1 && !g.ws) return hipErrorInvalidValue;
   if (ak == AK_I8) {
     switch (epi) {

@@ -88,8 +88,8 @@ struct QGemmArgs {
   int tiles_m;                            // set by the launcher
 };
 bool gemm_q_ok(int akind, int bkind, int epi, int m, int n, int k);
-size_t gemm_q_ws_bytes(int akind, int epi, int m, int n, int k);
-int gemm_q_splits(int akind, int epi, int m, int n, int k);
+size_t gemm_q_ws_bytes(int akind, int bkind, int epi, int m, int n, int k);
+int gemm_q_splits(int akind, int bkind, int epi, int m, int n, int k);
 hipError_t launch_gemm_q(int akind, int bkind, int epi, const QGemmArgs& g, hipStream_t st);
 // Grouped (MoE) form, MXFP4 weights and f16 activations only; g.m = the
 // largest group's rows, epi EPI_SWIGLU_F16 or EPI_STORE_F16, no split K.

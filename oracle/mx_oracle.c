@@ -405,17 +405,31 @@ static void deq_row_fmt(int fmt, const uint8_t *q, const void *s, int row, int k
     }
 }
 
+/* Accumulation of the dequantized dot products: float64 (the oracle, the
+ * default) or float32 in K order (BASELINE's CPU-baseline semantics, used
+ * only to time that baseline).  Process-wide; set before a call. */
+static int g_accum_f32 = 0;
+
+void orc_set_accum_f32(int on) { g_accum_f32 = on != 0; }
+
 static void *rowjob_run(void *arg)
 {
     rowjob_t *j = (rowjob_t *)arg;
     float *w = (float *)malloc(sizeof(float) * (size_t)j->k);
+    const int f32 = g_accum_f32;
     for (int r = j->r0; r < j->r1; r++) {
         deq_row_fmt(j->fmt, j->q, j->s, r, j->k, w);
         for (int t = 0; t < j->n_tok; t++) {
             const float *a = j->act + (size_t)t * j->k;
-            double acc = 0.0;
-            for (int i = 0; i < j->k; i++) acc += (double)a[i] * (double)w[i];
-            j->out[(size_t)t * j->n_rows + r] = (float)acc;
+            if (f32) {
+                float acc = 0.0f;
+                for (int i = 0; i < j->k; i++) acc += a[i] * w[i];
+                j->out[(size_t)t * j->n_rows + r] = acc;
+            } else {
+                double acc = 0.0;
+                for (int i = 0; i < j->k; i++) acc += (double)a[i] * (double)w[i];
+                j->out[(size_t)t * j->n_rows + r] = (float)acc;
+            }
         }
     }
     free(w);
@@ -555,19 +569,49 @@ void orc_quant_int8_per_token(const float *x, int tokens, int k, int8_t *q, floa
 }
 
 /* W8A8 rows: out[t][r] = (sum_i qx[t][i] * qw[r][i]) * sx[t] * sw[r], the
- * int32-accumulate row of MP:61-70 with per-token/per-row scales. */
-static void w8a8_gemm(const int8_t *qx, const float *sx, int n_tok, const uint8_t *qw,
-                      const float *sw, int n_rows, int k, float *out)
+ * int32-accumulate row of MP:61-70 with per-token/per-row scales.  Exact
+ * integer sums, so the split of the rows over threads changes nothing. */
+typedef struct {
+    const int8_t *qx; const float *sx; int n_tok;
+    const uint8_t *qw; const float *sw; int n_rows, k;
+    float *out;
+    int r0, r1;
+} w8a8job_t;
+
+static void *w8a8_run(void *arg)
 {
-    for (int r = 0; r < n_rows; r++) {
-        const int8_t *wr = (const int8_t *)qw + (size_t)r * k;
-        for (int t = 0; t < n_tok; t++) {
-            const int8_t *xr = qx + (size_t)t * k;
+    const w8a8job_t *j = (const w8a8job_t *)arg;
+    for (int r = j->r0; r < j->r1; r++) {
+        const int8_t *wr = (const int8_t *)j->qw + (size_t)r * j->k;
+        for (int t = 0; t < j->n_tok; t++) {
+            const int8_t *xr = j->qx + (size_t)t * j->k;
             int64_t acc = 0;
-            for (int i = 0; i < k; i++) acc += (int32_t)xr[i] * (int32_t)wr[i];
-            out[(size_t)t * n_rows + r] = (float)acc * sx[t] * sw[r];
+            for (int i = 0; i < j->k; i++) acc += (int32_t)xr[i] * (int32_t)wr[i];
+            j->out[(size_t)t * j->n_rows + r] = (float)acc * j->sx[t] * j->sw[r];
         }
     }
+    return NULL;
+}
+
+static void w8a8_gemm(const int8_t *qx, const float *sx, int n_tok, const uint8_t *qw,
+                      const float *sw, int n_rows, int k, float *out, int threads)
+{
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    pthread_t th[256];
+    w8a8job_t jobs[256];
+    int per = (n_rows + threads - 1) / threads, started = 0;
+    for (int t = 0; t < threads; t++) {
+        w8a8job_t *j = &jobs[t];
+        j->qx = qx; j->sx = sx; j->n_tok = n_tok; j->qw = qw; j->sw = sw; j->n_rows = n_rows; j->k = k;
+        j->out = out;
+        j->r0 = t * per; j->r1 = (t + 1) * per > n_rows ? n_rows : (t + 1) * per;
+        if (j->r0 >= j->r1) break;
+        if (threads == 1) { w8a8_run(j); break; }
+        pthread_create(&th[t], NULL, w8a8_run, j);
+        started++;
+    }
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
 }
 
 void orc_mlp_format(int fmt, int tokens, int hidden, int inter, const uint16_t *x,
@@ -591,11 +635,11 @@ void orc_mlp_format(int fmt, int tokens, int hidden, int inter, const uint16_t *
         int8_t *qx = (int8_t *)malloc((size_t)n_sel * (hidden > inter ? hidden : inter));
         float *sx = (float *)malloc(sizeof(float) * (size_t)n_sel);
         orc_quant_int8_per_token(xa, n_sel, hidden, qx, sx);
-        w8a8_gemm(qx, sx, n_sel, qg, (const float *)sg, inter, hidden, g);
-        w8a8_gemm(qx, sx, n_sel, qu, (const float *)su, inter, hidden, u);
+        w8a8_gemm(qx, sx, n_sel, qg, (const float *)sg, inter, hidden, g, threads);
+        w8a8_gemm(qx, sx, n_sel, qu, (const float *)su, inter, hidden, u, threads);
         orc_swiglu_float(g, u, cnt, mid);
         orc_quant_int8_per_token(mid, n_sel, inter, qx, sx);
-        w8a8_gemm(qx, sx, n_sel, qd, (const float *)sd, hidden, inter, o);
+        w8a8_gemm(qx, sx, n_sel, qd, (const float *)sd, hidden, inter, o, threads);
         free(qx);
         free(sx);
     } else {

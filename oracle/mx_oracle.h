@@ -73,6 +73,12 @@ void orc_swiglu_i8(const int32_t *gate, const int32_t *up, size_t count, int8_t 
  * rows_sel: token indices to evaluate (NULL = all tokens); out has
  * n_sel x hidden entries (f16 bits for modes 0/1, f32 for mode 2).
  * threads: worker threads (>=1). */
+/* Dot products of orc_mlp_mxfp4 / orc_mlp_format (except W8A8, which is
+ * integer) accumulate in float64 by default; on != 0 switches to float32 in
+ * K order, BASELINE's CPU-baseline semantics (bench.py's cpu_baseline leg
+ * only; the tests keep float64).  Process-wide. */
+void orc_set_accum_f32(int on);
+
 void orc_mlp_mxfp4(int mode, int tokens, int hidden, int inter, const uint16_t *x,
                    const uint8_t *wg, const uint8_t *sg, const uint8_t *wu, const uint8_t *su,
                    const uint8_t *wd, const uint8_t *sd, const int *rows_sel, int n_sel,

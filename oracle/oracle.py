@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
             "orc_swiglu_float": (None, [_vp, _vp, _sz, _vp]),
             "orc_swiglu_half": (None, [_vp, _vp, _sz, _vp]),
             "orc_swiglu_i8": (None, [_vp, _vp, _sz, _vp]),
+            "orc_set_accum_f32": (None, [_int]),
             "orc_mlp_mxfp4": (None, [_int, _int, _int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _int, _vp, _int]),
             "orc_quant_rowwise": (None, [_int, _vp, _int, _int, _vp, _vp]),
@@ -190,6 +191,12 @@ def mlp_mxfp4(mode: int, x: np.ndarray, wg, sg, wu, su, wd, sd, hidden: int, int
     lib().orc_mlp_mxfp4(mode, tokens, hidden, inter, _p(xb), _p(wg), _p(sg), _p(wu), _p(su),
                         _p(wd), _p(sd), _p(sel), n_sel, _p(out), threads)
     return out if mode == MLP_REFROW else out.view(np.float16)
+
+
+def set_accum_f32(on: bool) -> None:
+    """float32 (True) or float64 (False, the default) dot-product accumulation
+    in mlp_mxfp4 / mlp_format; float32 only for timing the CPU baseline."""
+    lib().orc_set_accum_f32(1 if on else 0)
 
 
 def quant_rowwise(fmt: int, w: np.ndarray):

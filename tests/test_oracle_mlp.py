@@ -232,3 +232,25 @@ def test_format_mlp_vs_numpy():
         rel, cos = O.mlp_error(out, ref)
         tol = 5e-2 if fmt == O.WF_W8A8 else O.MAX_ABS_REL_TOL
         assert rel <= tol and cos >= 0.999, (fmt, rel, cos)
+
+
+def test_accum_f32_switch():
+    """The CPU-baseline switch (float32 accumulation in K order) stays within
+    float32 rounding of the float64 oracle, differs from it in some bits at
+    K = 4096, and is off again afterwards (the tests use float64)."""
+    rng = np.random.default_rng(21)
+    T, H, I = 4, 4096, 256
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    qs = []
+    for n, k in ((I, H), (I, H), (H, I)):
+        qs += list(O.mxfp4_quantize(rng.normal(0, 0.02, (n, k)).astype(np.float32)))
+    f64 = O.mlp_mxfp4(O.MLP_F16, x, *qs, H, I)
+    O.set_accum_f32(True)
+    try:
+        f32 = O.mlp_mxfp4(O.MLP_F16, x, *qs, H, I, threads=4)
+    finally:
+        O.set_accum_f32(False)
+    rel, cos = O.mlp_error(f32, f64)
+    assert rel < 2e-3 and cos > 0.99999, (rel, cos)
+    assert not np.array_equal(f32.view(np.uint16), f64.view(np.uint16))
+    assert np.array_equal(O.mlp_mxfp4(O.MLP_F16, x, *qs, H, I).view(np.uint16), f64.view(np.uint16))
