@@ -187,7 +187,13 @@ constexpr int out_bytes(int epi) {
 // stages in flight, for launches of at most one workgroup per CU, which
 // otherwise sit in the DMA latency of every stage (8-bit / f16 weights,
 // BCH = 1 only).
-template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2>
+// SCL (4-bit weights): the E8M0 / f16 scales of the workgroup's weight rows
+// over its whole K range are copied into LDS before the loop (at most
+// kScLds bytes) and read from there per stage.  Loaded per stage from global
+// memory instead, each stage waits for loads issued one stage earlier, whose
+// latency the short stages do not cover.
+constexpr int kScLds = 16384;
+template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2, bool SCL = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
   constexpr bool DUAL = is_dual(EPI);
@@ -304,6 +310,25 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 
   uint32_t scv[2][NWB];  // 4-bit scales of the stage in flight / in use
 
+  // SCL: the scale block [TBR rows][KT * KS/32 entries] into LDS, 2 bytes at a
+  // time (rows and entries are 2-byte aligned), before any DMA is issued.
+  constexpr int ESZ = BK == BK_INT4G32 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? kScLds : 16];
+  const int sc_row = KT * (KS / 32) * ESZ;  // bytes of one row's scales
+  if constexpr (SCL) {
+    static_assert(SCALES4, "scales in LDS are for 4-bit weights");
+    const int units = TBR * sc_row / 2;
+    for (int i = tid; i < units; i += 256) {
+      const int tr = i / (sc_row / 2), c = i % (sc_row / 2);
+      const int wrow = DUAL ? n0 + (tr & 63) : n0 + tr;
+      const uint8_t* sb = reinterpret_cast<const uint8_t*>(DUAL && tr >= 64 ? g.s1 : g.s0);
+      const uint16_t v = *reinterpret_cast<const uint16_t*>(
+          sb + ((size_t)wrow * (K / 32) + (size_t)kt0 * (KS / 32)) * ESZ + (size_t)c * 2);
+      *reinterpret_cast<uint16_t*>(sc_lds + tr * sc_row + c * 2) = v;
+    }
+    __syncthreads();
+  }
+
   // A of stage S into slot AS; the 4-bit scales of stage S into register set P.
 #define MXQ_DMA_A(S, AS)                                                                           \
   {                                                                                                \
@@ -313,7 +338,12 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   }
 #define MXQ_SCALES(S, P)                                                                           \
   {                                                                                                \
-    if (SCALES4) {                                                                                 \
+    if constexpr (SCL) {                                                                           \
+      _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
+        const uint8_t* p_ = sc_lds + (b_blk[j] + r32) * sc_row + ((S) * (KS / 32) + h) * ESZ;     \
+        scv[P][j] = ESZ == 2 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_;  \
+      }                                                                                            \
+    } else if (SCALES4) {                                                                          \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
         const uint8_t* p_ = sc_src[j] + (size_t)(S) * (KS / 32) * (BK == BK_INT4G32 ? 2 : 1);     \
         scv[P][j] = BK == BK_INT4G32 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_; \
@@ -332,7 +362,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     }                                                                                              \
   }
   // loads one wave issues per stage (A + scales); a B chunk adds NB
-  constexpr int VM_A = NA + (SCALES4 ? NWB : 0);
+  constexpr int VM_A = NA + (SCALES4 && !SCL ? NWB : 0);
 
   // One stage's MFMAs, in two halves.  MXQ_READ issues every LDS fragment
   // read of the stage into registers (AR, BR); MXQ_MATH widens the weights
@@ -365,7 +395,24 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       }                                                                                            \
     }                                                                                              \
   }
+  // MXFP4 weights: E8M0 byte 255 (+inf to the reference, NaN to the
+  // hardware) needs the exact decode, which costs ~25 VALU instructions per
+  // 8 values.  Left per lane, the compiler computes both decodes and selects
+  // (~450 VALU per stage against 16 MFMAs); instead a ballot over the
+  // stage's scale bytes picks one whole-stage form, the exact one only when
+  // some lane's block has byte 255.
 #define MXQ_MATH(AR, BR, P)                                                                        \
+  {                                                                                                \
+    bool exact_ = false;                                                                           \
+    if constexpr (BK == BK_MXFP4) {                                                                \
+      uint32_t hit_ = 0;                                                                           \
+      _Pragma("unroll") for (int j = 0; j < NWB; j++) hit_ |= scv[P][j] == 255u;                    \
+      exact_ = __ballot(hit_ != 0) != 0;                                                           \
+    }                                                                                              \
+    if (__builtin_expect(exact_, 0)) MXQ_MATH_FORM(AR, BR, P, true)                                \
+    else MXQ_MATH_FORM(AR, BR, P, false)                                                           \
+  }
+#define MXQ_MATH_FORM(AR, BR, P, EXACT)                                                            \
   {                                                                                                \
     _Pragma("unroll") for (int s = 0; s < KSTEPS; s++) {                                           \
       if constexpr (AK == AK_I8) {                                                                 \
@@ -391,7 +438,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
             bf[j] = __builtin_bit_cast(v8h, BR[s][j]);                                             \
           } else if constexpr (BK == BK_MXFP4 || BK == BK_INT4G32) {                               \
             const v4i w_ = BR[0][j];                                                               \
-            if (BK == BK_MXFP4) bf[j] = fp4x8_dequant_f16(w_[s], scv[P][j]);                       \
+            if (BK == BK_MXFP4) bf[j] = (EXACT) ? fp4x8_dequant_f16(w_[s], scv[P][j])               \
+                                                : fp4x8_to_f16x8(w_[s], e8m0_as_cvt_scale(scv[P][j])); \
             else bf[j] = i4x8_to_f16(w_[s], __builtin_bit_cast(_Float16, (uint16_t)scv[P][j]));    \
           } else {                                                                                 \
             const v4i w_ = BR[s >> 1][j];                                                          \
@@ -535,6 +583,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 #undef MXQ_DMA_B
 #undef MXQ_SCALES
 #undef MXQ_COMPUTE
+#undef MXQ_MATH_FORM
+#undef MXQ_MATH
+#undef MXQ_READ
 
   // ---- epilogue, or the raw partial tile when K is split (separate loops
   // behind one uniform branch).
@@ -689,6 +740,11 @@ template <int AK, int BK> constexpr int b_chunk() {
   return (BK == BK_MXFP4 || BK == BK_INT4G32) ? 128 / b_row_bytes<BK>(AInfo<AK>::KS) : 1;
 }
 
+// True when a workgroup's scales over kt stages fit the LDS copy (SCL).
+template <int AK, int BK, int NWB> bool sc_lds_fits(int kt) {
+  return NWB * 64 * kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1) <= kScLds;
+}
+
 // Launches of at most this many workgroups (one per CU) take the deep ring,
 // for weight formats staged per stage whose four slots fit the 160 KB of LDS
 // (not f32 activations x f16 weights: 4 x 48 KB).
@@ -723,10 +779,16 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
       return hipGetLastError();
     }
   }
-  if (BC > 1 && kt % BC == 0 && kt >= 4 * BC)
-    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
-  else
-    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0, st, g, 0);
+  const dim3 grid(g.tiles_m * tiles_n, splits);
+  constexpr bool S4 = BK == BK_MXFP4 || BK == BK_INT4G32;
+  const bool scl = S4 && sc_lds_fits<AK, BK, NWB>(kt);
+  if (BC > 1 && kt % BC == 0 && kt >= 4 * BC) {
+    if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC, 2, S4>), grid, dim3(256), 0, st, g, 0);
+    else hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC>), grid, dim3(256), 0, st, g, 0);
+  } else {
+    if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 2, S4>), grid, dim3(256), 0, st, g, 0);
+    else hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1>), grid, dim3(256), 0, st, g, 0);
+  }
   if (splits > 1) {
     const size_t n = (size_t)g.m * g.n;
     hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st, g, splits);
@@ -749,12 +811,16 @@ hipError_t launch_q_grouped(const QGemmArgs& g0, const GroupTable& gt, int group
   g.tiles_m = (g.m + kTM - 1) / kTM;
   const int tiles_n = is_dual(EPI) ? g.n / 64 : g.n / (NWB * 64);
   constexpr int BC = b_chunk<AK, BK>();
-  if (BC > 1 && (g.k / AInfo<AK>::KS) % BC == 0 && g.k / AInfo<AK>::KS >= 4 * BC)
-    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, BC>), dim3(g.tiles_m * tiles_n, 1, groups), dim3(256), 0, st,
-                       g, gt);
-  else
-    hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, 1>), dim3(g.tiles_m * tiles_n, 1, groups), dim3(256), 0, st,
-                       g, gt);
+  const int kt = g.k / AInfo<AK>::KS;
+  const dim3 grid(g.tiles_m * tiles_n, 1, groups);
+  const bool scl = sc_lds_fits<AK, BK, NWB>(kt);  // MXFP4 only here
+  if (BC > 1 && kt % BC == 0 && kt >= 4 * BC) {
+    if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, BC, 2, true>), grid, dim3(256), 0, st, g, gt);
+    else hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, BC>), grid, dim3(256), 0, st, g, gt);
+  } else {
+    if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, 1, 2, true>), grid, dim3(256), 0, st, g, gt);
+    else hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, 1>), grid, dim3(256), 0, st, g, gt);
+  }
   return hipGetLastError();
 }
 
