@@ -519,6 +519,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 #define MXQ_DEEP(U, CUR, NXT)                                                                      \
   {                                                                                                \
     const int st_ = kt + (U);                                                                      \
+    /* the previous stage's MFMAs stay ahead of this wait: moved past it, they */                  \
+    /* would leave the next stage's LDS reads nothing to overlap */                                \
+    __builtin_amdgcn_sched_barrier(0);                                                             \
     if (b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm((NS - 2) * (VM_A + NB)) & ~(15 << 8));        \
     else __builtin_amdgcn_s_waitcnt(wait_vm((NS - 2) * VM_A) & ~(15 << 8));                        \
     __builtin_amdgcn_s_barrier();                                                                  \
