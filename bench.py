@@ -314,13 +314,17 @@ def main():
                               cpu=cpu and 64)
             r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
             sec["c4_w4a4"] = r
-        for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_W4A4, "w4a4")):
+        for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_W4A4, "w4a4"),
+                       (M.MLP_SCALED, "scaled")):
             if not want("c0", tag):
                 continue
             r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, 24, 100, 10, seed=5,
                               cpu=cpu and tag == "fused" and 128)
             sec[f"c0_{tag}"] = r
-        for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant")):
+        # the scaled row runs two FP8 x FP4 MFMAs per block (x split in two
+        # E4M3 terms): the MFMA time of one f16 MFMA, so its useful FLOP/s are
+        # held to the same f16 peak
+        for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_SCALED, "scaled")):
             if not want("c2", tag):
                 continue
             r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, 24, 100, 10, seed=6,

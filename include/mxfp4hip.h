@@ -63,7 +63,16 @@ enum {
   /* reference fused-row epilogue: swiglu_half (x1/16, clamp +-20, mid half),
    * f32 out (encodeMXFP4FusedMLP main.swift:2033-2135 + MPPMLPKernels.metal:204-220);
    * reproduces the reference checksum 403573 (README.md:292-294). */
-  MX_MLP_REFROW = 3
+  MX_MLP_REFROW = 3,
+  /* scaled: the native scale-plane rows (MXFP4Kernels.metal:138-173) on the
+   * CDNA4 scaled MFMA: x and mid are split into two FP8 E4M3 terms with an
+   * E8M0 pair per 64 K (relative error <= 2^-8 per value), and
+   * v_mfma_scale_f32_32x32x64_f8f6f4 takes the FP4 codes and their E8M0
+   * bytes directly, two MFMAs per block.  One more launch (the split of x).
+   * E8M0 byte 255 and non-finite activations give NaN products (the
+   * hardware's reading), where the other variants keep the reference's
+   * +inf scale. */
+  MX_MLP_SCALED = 4
 };
 
 /* Weight-format rows (MPP/NAX rows main.swift:945-1042, 1247-1413;

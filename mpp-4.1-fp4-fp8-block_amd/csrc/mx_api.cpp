@@ -111,7 +111,7 @@ int check_mlp_cfg(mx_ctx* c, int variant, const mx_mlp_config* cfg) {
     return set_err(c, MX_EINVAL, "hidden and intermediate must be multiples of 64 (MFMA tile).");
   if (variant == MX_MLP_W4A4 && (H % 128 || I % 128))
     return set_err(c, MX_EINVAL, "W4A4 needs hidden and intermediate to be multiples of 128.");
-  if (variant < MX_MLP_FUSED || variant > MX_MLP_REFROW)
+  if (variant < MX_MLP_FUSED || variant > MX_MLP_SCALED)
     return set_err(c, MX_EINVAL, "Unknown MLP variant %d.", variant);
   return MX_OK;
 }
@@ -126,13 +126,14 @@ bool gemv_ok(const mx_mlp_config* cfg) {
 }
 
 // Which kernels a forward runs (shared by the launcher and the name query).
-enum MlpPath { PATH_GEMV, PATH_GEMM_Q, PATH_REFROW, PATH_DEQUANT, PATH_W4A4 };
+enum MlpPath { PATH_GEMV, PATH_GEMM_Q, PATH_REFROW, PATH_DEQUANT, PATH_W4A4, PATH_SCALED };
 
 MlpPath mlp_path(int variant, const mx_mlp_config* cfg) {
   switch (variant) {
     case MX_MLP_FUSED: return gemv_ok(cfg) ? PATH_GEMV : PATH_GEMM_Q;
     case MX_MLP_REFROW: return PATH_REFROW;
     case MX_MLP_DEQUANT: return PATH_DEQUANT;
+    case MX_MLP_SCALED: return PATH_SCALED;
     default: return PATH_W4A4;
   }
 }
@@ -142,6 +143,7 @@ struct MlpScratch {
   size_t mid = 0, gate = 0, up = 0, wg = 0, wu = 0, wd = 0, xq = 0, xs = 0, mq = 0, ms = 0;
   size_t sg = 0, su = 0, sd = 0;  // stage-major weight scale copies (W4A4)
   size_t qws = 0;                 // split-K partials of the small-M GEMMs
+  size_t xe = 0, me = 0;          // F8X2 scale pairs of x and mid (MX_MLP_SCALED)
   size_t total = 0;
 };
 
@@ -155,6 +157,13 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
     const int e = variant == MX_MLP_REFROW ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16;
     s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_MXFP4, e, (int)T, (int)I, (int)H),
                           mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_MXFP4, mx::EPI_STORE_F32, (int)T, (int)H, (int)I)));
+  } else if (variant == MX_MLP_SCALED) {
+    s.xq = take(mx::f8x2_data_bytes(T, H));
+    s.xe = take(mx::f8x2_e8_bytes(T, H));
+    s.mq = take(mx::f8x2_data_bytes(T, I));
+    s.me = take(mx::f8x2_e8_bytes(T, I));
+    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F8X2, mx::BK_MXFP4, mx::EPI_SWIGLU_F8X2, (int)T, (int)I, (int)H),
+                          mx::gemm_q_ws_bytes(mx::AK_F8X2, mx::BK_MXFP4, mx::EPI_STORE_F16, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_DEQUANT) {
     s.wg = take(I * H * 2);
     s.wu = take(I * H * 2);
@@ -242,6 +251,24 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
                      [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_MXFP4, e_gu, gu, st); }});
     steps.push_back({ref ? "gemm_q_mxfp4_down_f32" : "gemm_q_mxfp4_down",
                      [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_MXFP4, e_dn, dn, st); }});
+  } else if (path == PATH_SCALED) {
+    // x and mid as two E4M3 terms with E8M0 pairs per 64 K (F8X2), both
+    // GEMMs on v_mfma_scale_f32_32x32x64_f8f6f4 with the weights' FP4 codes
+    // and E8M0 bytes as the B operand and its scales
+    uint8_t* xq = ws + s.xq;
+    uint32_t* xe = reinterpret_cast<uint32_t*>(ws + s.xe);
+    uint8_t* mq = ws + s.mq;
+    uint32_t* me = reinterpret_cast<uint32_t*>(ws + s.me);
+    void* qws = ws + s.qws;
+    mx::QGemmArgs gu{xq, nullptr, wg, sg, wu, su, mq, qws, T, I, H, 0, xe, me};
+    mx::QGemmArgs dn{mq, nullptr, wd, sd, nullptr, nullptr, out, qws, T, H, I, 0, me, nullptr};
+    steps.push_back({"split_x_f8x2", [=] {
+                       return mx::launch_split_f8x2(static_cast<const uint16_t*>(x), T, H, xq, xe, st);
+                     }});
+    steps.push_back({"gemm_q_scaled_gate_up_swiglu",
+                     [=] { return mx::launch_gemm_q(mx::AK_F8X2, mx::BK_MXFP4, mx::EPI_SWIGLU_F8X2, gu, st); }});
+    steps.push_back({"gemm_q_scaled_down",
+                     [=] { return mx::launch_gemm_q(mx::AK_F8X2, mx::BK_MXFP4, mx::EPI_STORE_F16, dn, st); }});
   } else if (path == PATH_DEQUANT) {
     uint16_t* wg16 = reinterpret_cast<uint16_t*>(ws + s.wg);
     uint16_t* wu16 = reinterpret_cast<uint16_t*>(ws + s.wu);
@@ -719,13 +746,15 @@ const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index)
   static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
                               "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
   static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down", "w4a4_down_inf"};
-  if (index < 0 || !cfg || variant < MX_MLP_FUSED || variant > MX_MLP_REFROW) return nullptr;
+  static const char* sc[] = {"split_x_f8x2", "gemm_q_scaled_gate_up_swiglu", "gemm_q_scaled_down"};
+  if (index < 0 || !cfg || variant < MX_MLP_FUSED || variant > MX_MLP_SCALED) return nullptr;
   switch (mlp_path(variant, cfg)) {
     case PATH_GEMV: return index < 2 ? gemv[index] : nullptr;
     case PATH_GEMM_Q: return index < 2 ? fused[index] : nullptr;
     case PATH_REFROW: return index < 2 ? ref[index] : nullptr;
     case PATH_DEQUANT: return index < 7 ? deq[index] : nullptr;
     case PATH_W4A4: return index < 4 ? w4[index] : nullptr;
+    case PATH_SCALED: return index < 3 ? sc[index] : nullptr;
   }
   return nullptr;
 }

@@ -114,6 +114,93 @@ __device__ __forceinline__ uint32_t mxfp4_scale_byte(uint32_t amax_bits) {
   return (uint32_t)(s + 127);
 }
 
+// F8X2 term scale of a group with amax bits `amax_bits` (finite, > 0): the
+// smallest power of two s with amax <= 448 s (the E4M3 maximum, so no code
+// saturates), as an E8M0 byte (clamped at 2^-127).
+__device__ __forceinline__ uint32_t f8x2_scale_byte(uint32_t amax_bits) {
+  const uint32_t e = amax_bits >> 23;
+  const int fl = e ? (int)e - 127 : (31 - __builtin_clz(amax_bits)) - 149;
+  int s = fl - 8 + ((e && (amax_bits & 0x7fffffu) > 0x600000u) ? 1 : 0);
+  if (s < -127) s = -127;
+  return (uint32_t)(s + 127);
+}
+
+// F8X2 split (layout in mx_internal.h) of one (row, 64-K group), held by L
+// consecutive lanes (L = 2, 4, 8 or 16; the group starts at a lane index
+// that is a multiple of L): lane j = lane % L holds the V = 64 / L values of
+// k [V j, V j + V) in v.  t1 = RNE_E4M3(v / s1); the residual r = v - t1 s1
+// is exact in f32; t2 = RNE_E4M3(r / s2), each s from its term's group
+// maximum.  A group with a non-finite value gets scale bytes 255 (its
+// products are NaN) and NaN codes; an all-zero group gets bytes 127 and zero
+// codes.  All L lanes must be active (they exchange maxima).  Writes the
+// lane's bytes of both terms into the group's 128 bytes at `grp` and, from
+// lane j = 0, the scale dword at `e8`.
+template <int L>
+__device__ __forceinline__ void f8x2_split_store(const float* v, int j, uint8_t* grp, uint32_t* e8) {
+  constexpr int V = 64 / L, D = V / 4;  // values and dwords per lane and term
+  static_assert(L >= 2 && L <= 16 && (L & (L - 1)) == 0, "2..16 lanes per group");
+  uint32_t am = 0;
+#pragma unroll
+  for (int k = 0; k < V; k++) am = max(am, __builtin_bit_cast(uint32_t, v[k]) & 0x7fffffffu);
+#pragma unroll
+  for (int o = 1; o < L; o <<= 1) am = max(am, (uint32_t)__shfl_xor((int)am, o));
+  uint32_t t1[D], t2[D];
+  uint32_t b1 = 127u, b2 = 127u;
+  if (am >= 0x7f800000u) {
+    b1 = b2 = 255u;
+#pragma unroll
+    for (int d = 0; d < D; d++) t1[d] = t2[d] = 0x7f7f7f7fu;
+  } else {
+#pragma unroll
+    for (int d = 0; d < D; d++) t1[d] = t2[d] = 0u;
+    float r[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) r[k] = v[k];
+    if (am != 0u) {
+      b1 = f8x2_scale_byte(am);
+      const float sc1 = e8m0_as_cvt_scale(b1);
+      uint32_t am2 = 0;
+#pragma unroll
+      for (int d = 0; d < D; d++) {
+        v2s w = {0, 0};
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * d], v[4 * d + 1], sc1, false);
+        w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, v[4 * d + 2], v[4 * d + 3], sc1, true);
+        t1[d] = __builtin_bit_cast(uint32_t, w);
+        const v2f lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(t1[d], sc1, false);
+        const v2f hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(t1[d], sc1, true);
+        r[4 * d] = v[4 * d] - lo[0];
+        r[4 * d + 1] = v[4 * d + 1] - lo[1];
+        r[4 * d + 2] = v[4 * d + 2] - hi[0];
+        r[4 * d + 3] = v[4 * d + 3] - hi[1];
+#pragma unroll
+        for (int t = 0; t < 4; t++) am2 = max(am2, __builtin_bit_cast(uint32_t, r[4 * d + t]) & 0x7fffffffu);
+      }
+#pragma unroll
+      for (int o = 1; o < L; o <<= 1) am2 = max(am2, (uint32_t)__shfl_xor((int)am2, o));
+      if (am2 != 0u) {
+        b2 = f8x2_scale_byte(am2);
+        const float sc2 = e8m0_as_cvt_scale(b2);
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+          v2s w = {0, 0};
+          w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, r[4 * d], r[4 * d + 1], sc2, false);
+          w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, r[4 * d + 2], r[4 * d + 3], sc2, true);
+          t2[d] = __builtin_bit_cast(uint32_t, w);
+        }
+      }
+    }
+  }
+  // k -> byte (k & 15) + 16 * {0, 2, 1, 3}[k / 16] within a term
+#pragma unroll
+  for (int d = 0; d < D; d++) {
+    const int k0 = V * j + 4 * d, q = k0 >> 4;
+    const int pos = (k0 & 15) + 16 * (q == 1 ? 2 : q == 2 ? 1 : q);
+    *reinterpret_cast<uint32_t*>(grp + pos) = t1[d];
+    *reinterpret_cast<uint32_t*>(grp + 64 + pos) = t2[d];
+  }
+  if (j == 0) *e8 = b1 | (b2 << 8);
+}
+
 // Quantize 8 consecutive f32 values into one dword of 8 FP4 codes with the
 // block scale byte `sb` (0..254): code = RNE(x / 2^(sb-127)), saturating.
 __device__ __forceinline__ uint32_t fp4x8_from_f32(const float* v, uint32_t sb) {

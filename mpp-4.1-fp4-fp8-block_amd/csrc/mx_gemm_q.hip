@@ -54,6 +54,7 @@ template <int AK> struct AInfo;
 template <> struct AInfo<AK_F16> { static constexpr int KS = 64, RB = 128; };
 template <> struct AInfo<AK_F32> { static constexpr int KS = 64, RB = 256; };
 template <> struct AInfo<AK_I8> { static constexpr int KS = 128, RB = 128; };
+template <> struct AInfo<AK_F8X2> { static constexpr int KS = 64, RB = 128; };  // 2 terms x 64 B
 
 // bytes of one weight row per stage
 template <int BK> constexpr int b_row_bytes(int ks) {
@@ -75,6 +76,9 @@ __device__ __forceinline__ int swz(int row) {
 // kernel's launch stub.
 __device__ __forceinline__ void dma16(const void* src, void* lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
 }
 
 // s_waitcnt immediate (gfx9 encoding): vmcnt(n) only.
@@ -156,7 +160,7 @@ __device__ __forceinline__ void epi_store(void* c, size_t o, float x0, float u) 
 }
 
 constexpr bool is_dual(int epi) {
-  return epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_HALF || epi == EPI_SWIGLU_F32;
+  return epi == EPI_SWIGLU_F16 || epi == EPI_SWIGLU_HALF || epi == EPI_SWIGLU_F32 || epi == EPI_SWIGLU_F8X2;
 }
 constexpr bool row_scaled(int bk) { return bk == BK_E4M3 || bk == BK_E5M2 || bk == BK_INT8 || bk == BK_I8; }
 
@@ -193,6 +197,9 @@ constexpr int out_bytes(int epi) {
 // memory instead, each stage waits for loads issued one stage earlier, whose
 // latency the short stages do not cover.
 constexpr int kScLds = 16384;
+// F8X2 activations give 2 KB of it to the A slots' scale pairs, so that two
+// workgroups still share a CU (80 KB each).
+constexpr int sc_lds_bytes(int ak) { return ak == AK_F8X2 ? kScLds - 2048 : kScLds; }
 template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2, bool SCL = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
@@ -231,7 +238,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // one slot does not write what the fragment reads of another slot read.
   // (Its wait insertion tells at most eight DMA targets apart, so the deep
   // ring keeps A and B of a slot in one array: four targets.)
-  constexpr int SA = NS == 2 ? kTM * RA : 16, SB = NS == 2 ? TBR * RBC : 16;
+  // F8X2 activations: the A slot also holds the stage's E8M0 pairs of the
+  // 128 tile rows (512 B) and a spare 512 B that waves 2 and 3 fill with
+  // the same dwords, so that every wave issues the same loads per stage.
+  constexpr int SA = NS == 2 ? kTM * RA + (AK == AK_F8X2 ? 1024 : 0) : 16, SB = NS == 2 ? TBR * RBC : 16;
   constexpr int SD = NS > 2 ? kTM * RA + TBR * RBC : 16;
   __shared__ __attribute__((aligned(16))) uint8_t a_s0[SA];
   __shared__ __attribute__((aligned(16))) uint8_t a_s1[SA];
@@ -251,11 +261,16 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   const int n0 = DUAL ? nt * 64 : nt * TBR;  // first channel / weight row
   const int KT = K / KS / (int)gridDim.y;     // stages of this split
   const int kt0 = (int)blockIdx.y * KT;
-  const size_t a_row = (size_t)K * (AK == AK_F32 ? 4 : AK == AK_F16 ? 2 : 1);
+  const size_t a_row = (size_t)K * (AK == AK_F32 ? 4 : (AK == AK_F16 || AK == AK_F8X2) ? 2 : 1);
+  static_assert(AK != AK_F8X2 || (BK == BK_MXFP4 && NS == 2 && !GROUPED),
+                "F8X2 activations: MXFP4 weights on the scaled MFMA, 2-slot ring");
   const size_t b_row = (size_t)b_row_bytes<BK>(K);
 
   // ---- DMA sources (per lane, per instruction)
   constexpr int CA = RA / 16, CB = RBC / 16;  // 16-byte chunks per LDS row
+  // F8X2: this lane's row of the stage-major E8M0 pairs (waves 0 / 1: tile
+  // rows 64w + lane; waves 2 / 3 repeat them into the spare copy)
+  const uint32_t* ae_src = AK == AK_F8X2 ? g.a_e8 + min(m0 + (wave & 1) * 64 + lane, M - 1) : nullptr;
   const uint8_t* a_src[NA];
 #pragma unroll
   for (int q = 0; q < NA; q++) {
@@ -309,11 +324,12 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
 
   uint32_t scv[2][NWB];  // 4-bit scales of the stage in flight / in use
+  uint32_t asv[2] = {0u, 0u};  // F8X2: E8M0 pair of A blocks 0 / 1 for the stage in use
 
   // SCL: the scale block [TBR rows][KT * KS/32 entries] into LDS, 2 bytes at a
   // time (rows and entries are 2-byte aligned), before any DMA is issued.
   constexpr int ESZ = BK == BK_INT4G32 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? kScLds : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? sc_lds_bytes(AK) : 16];
   const int sc_row = KT * (KS / 32) * ESZ;  // bytes of one row's scales
   if constexpr (SCL) {
     static_assert(SCALES4, "scales in LDS are for 4-bit weights");
@@ -335,6 +351,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     const size_t ka_ = (size_t)(kt0 + (S)) * RA;                                                   \
     _Pragma("unroll") for (int q = 0; q < NA; q++)                                                 \
       dma16(a_src[q] + ka_, (AS) + (wave * NA + q) * 1024);                                         \
+    if constexpr (AK == AK_F8X2) dma4(ae_src + (size_t)(kt0 + (S)) * M, (AS) + kTM * RA + wave * 256); \
   }
 #define MXQ_SCALES(S, P)                                                                           \
   {                                                                                                \
@@ -362,7 +379,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     }                                                                                              \
   }
   // loads one wave issues per stage (A + scales); a B chunk adds NB
-  constexpr int VM_A = NA + (SCALES4 && !SCL ? NWB : 0);
+  constexpr int VM_A = NA + (SCALES4 && !SCL ? NWB : 0) + (AK == AK_F8X2 ? 1 : 0);
 
   // One stage's MFMAs, in two halves.  MXQ_READ issues every LDS fragment
   // read of the stage into registers (AR, BR); MXQ_MATH widens the weights
@@ -381,8 +398,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     _Pragma("unroll") for (int s = 0; s < KSTEPS; s++) {                                           \
       _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
         const int r_ = wm * 64 + i * 32 + r32;                                                     \
+        if (AK == AK_F8X2 && s == 0) asv[i] = *reinterpret_cast<const uint32_t*>((AS) + kTM * RA + r_ * 4); \
         _Pragma("unroll") for (int w = 0; w < AW; w++) {                                           \
-          const int ch_ = AK == AK_F32 ? 8 * h + 2 * s + w : 4 * h + s;                            \
+          /* F8X2: s = 2 * term + u, lane half h holds chunks 2h, 2h + 1 of each term */            \
+          const int ch_ = AK == AK_F32 ? 8 * h + 2 * s + w : AK == AK_F8X2 ? 4 * (s >> 1) + 2 * h + (s & 1) : 4 * h + s; \
           AR[s][i][w] = *reinterpret_cast<const v4i*>((AS) + r_ * RA + ((ch_ ^ swz<RA>(r_)) << 4)); \
         }                                                                                          \
       }                                                                                            \
@@ -401,8 +420,33 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // (~450 VALU per stage against 16 MFMAs); instead a ballot over the
   // stage's scale bytes picks one whole-stage form, the exact one only when
   // some lane's block has byte 255.
-#define MXQ_MATH(AR, BR, P)                                                                        \
+  // F8X2 activations: per A block i and weight block j, two
+  // v_mfma_scale_f32_32x32x64_f8f6f4 (A E4M3 term t with its E8M0 byte t
+  // of the pair, B FP4 with the lane's E8M0 byte) into one accumulator.
+  // Lane half h of both operands holds 32-block h of the stage, so the
+  // lane's own scale bytes are the ones each operand needs.
+#define MXQ_MATH_F8X2(AR, BR, P)                                                                   \
   {                                                                                                \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) {                                                \
+      v8i a1_, a2_;                                                                                \
+      _Pragma("unroll") for (int t = 0; t < 4; t++) {                                              \
+        a1_[t] = AR[0][i][0][t]; a1_[4 + t] = AR[1][i][0][t];                                      \
+        a2_[t] = AR[2][i][0][t]; a2_[4 + t] = AR[3][i][0][t];                                      \
+      }                                                                                            \
+      _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                            \
+        v8i b_;                                                                                    \
+        _Pragma("unroll") for (int t = 0; t < 4; t++) { b_[t] = BR[0][j][t]; b_[4 + t] = 0; }      \
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a1_, b_, (v16f)acc[i][j], 0, 4, 0, \
+                                                                    (int)asv[i], 0, (int)scv[P][j]); \
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a2_, b_, (v16f)acc[i][j], 0, 4, 1, \
+                                                                    (int)asv[i], 0, (int)scv[P][j]); \
+      }                                                                                            \
+    }                                                                                              \
+  }
+#define MXQ_MATH(AR, BR, P)                                                                        \
+  if constexpr (AK == AK_F8X2) {                                                                   \
+    MXQ_MATH_F8X2(AR, BR, P)                                                                       \
+  } else {                                                                                         \
     bool exact_ = false;                                                                           \
     if constexpr (BK == BK_MXFP4) {                                                                \
       uint32_t hit_ = 0;                                                                           \
@@ -587,6 +631,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 #undef MXQ_SCALES
 #undef MXQ_COMPUTE
 #undef MXQ_MATH_FORM
+#undef MXQ_MATH_F8X2
 #undef MXQ_MATH
 #undef MXQ_READ
 
@@ -630,6 +675,38 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
         else put(std::true_type{});
       }
     }
+    return;
+  }
+  if constexpr (EPI == EPI_SWIGLU_F8X2) {
+    // mid = silu(g) * u of the tile's 128 rows x 64 channels, which is one
+    // 64-K group of the down GEMM's F8X2 input, goes through LDS: wave
+    // (wm, wn) writes rows [64 wm, +64) x channels [32 wn, +32) into A slot
+    // wm (row r, channel c at r * 64 + (c ^ (r & 31)): the column writes and
+    // the row reads both spread over the banks), then lane pair p of the
+    // workgroup splits row p.
+    __syncthreads();
+    float* ml = reinterpret_cast<float*>(wm ? a_s1 : a_s0);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int rl = i * 32 + acc32_row(lane, v), c = wn * 32 + r32;
+        const float x0 = acc[i][0][v], u = acc[i][NWB - 1][v];
+        ml[rl * 64 + (c ^ (rl & 31))] = (x0 / (1.0f + expf(-x0))) * u;
+      }
+    __syncthreads();
+    const int pr = tid >> 1, half = tid & 1, rl = pr & 63;
+    const float* src = reinterpret_cast<const float*>(pr < 64 ? a_s0 : a_s1);
+    float mv[32];
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+      const int c = 32 * half + k;
+      mv[k] = src[rl * 64 + (c ^ (rl & 31))];
+    }
+    const int row = m0 + pr, grp = n0 / 64;
+    if (row < M)
+      f8x2_split_store<2>(mv, half, reinterpret_cast<uint8_t*>(g.c) + (size_t)row * 2 * g.n + (size_t)grp * 128,
+                          g.c_e8 + (size_t)grp * M + row);
     return;
   }
   // The scales are loaded up front, unconditionally (rows clamped), so the
@@ -692,6 +769,31 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
   constexpr bool DUAL = is_dual(EPI);
   constexpr int PL = DUAL ? 2 : 1;
   const size_t plane = (size_t)g.m * g.n;
+  if constexpr (EPI == EPI_SWIGLU_F8X2) {
+    // 16 lanes per (row, 64-channel group), 4 channels each; a group past
+    // the end exits as a whole
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int j = (int)(t & 15);
+    const int groups = g.n / 64;
+    const size_t gi = t >> 4;
+    if (gi >= (size_t)g.m * groups) return;
+    const int row = (int)(gi / groups), grp = (int)(gi % groups);
+    const size_t o = (size_t)row * g.n + (size_t)grp * 64 + 4 * j;
+    const float* w = reinterpret_cast<const float*>(g.ws);
+    float gs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, us[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < splits; k++) {
+      const float4 a = *reinterpret_cast<const float4*>(w + (size_t)(2 * k) * plane + o);
+      const float4 b = *reinterpret_cast<const float4*>(w + (size_t)(2 * k + 1) * plane + o);
+      gs[0] += a.x; gs[1] += a.y; gs[2] += a.z; gs[3] += a.w;
+      us[0] += b.x; us[1] += b.y; us[2] += b.z; us[3] += b.w;
+    }
+    float mv[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) mv[c] = (gs[c] / (1.0f + expf(-gs[c]))) * us[c];
+    f8x2_split_store<16>(mv, j, reinterpret_cast<uint8_t*>(g.c) + (size_t)row * 2 * g.n + (size_t)grp * 128,
+                         g.c_e8 + (size_t)grp * g.m + row);
+    return;
+  }
   const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (o >= plane) return;
   const int row = (int)(o / g.n), col = (int)(o % g.n);
@@ -745,7 +847,7 @@ template <int AK, int BK> constexpr int b_chunk() {
 
 // True when a workgroup's scales over kt stages fit the LDS copy (SCL).
 template <int AK, int BK, int NWB> bool sc_lds_fits(int kt) {
-  return NWB * 64 * kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1) <= kScLds;
+  return NWB * 64 * kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1) <= sc_lds_bytes(AK);
 }
 
 // Launches of at most this many workgroups (one per CU) take the deep ring,
@@ -757,6 +859,13 @@ constexpr bool deep_format(int ak, int bk) {
   const int ra = ak == AK_F32 ? 256 : 128;
   const int rb = bk == BK_F16 ? ks * 2 : ks;
   return bk != BK_MXFP4 && bk != BK_INT4G32 && 4 * 128 * (ra + rb) <= 160 * 1024;
+}
+
+// Workgroups of the split-K reduction: 4 outputs per thread (16 lanes per
+// (row, 64-channel group) for the F8X2 mid).
+template <int EPI> unsigned reduce_blocks(int m, int n) {
+  const size_t threads = (size_t)m * n / 4;
+  return (unsigned)((threads + 255) / 256);
 }
 
 template <int AK, int BK, int EPI, int NWB>
@@ -774,11 +883,9 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
     if (g.tiles_m * tiles_n * splits <= kDeepMaxWgs && kt >= 8 && kt % 4 == 0) {
       hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 4>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0,
                          st, g, 0);
-      if (splits > 1) {
-        const size_t n = (size_t)g.m * g.n;
-        hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st, g,
+      if (splits > 1)
+        hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3(reduce_blocks<EPI>(g.m, g.n)), dim3(256), 0, st, g,
                            splits);
-      }
       return hipGetLastError();
     }
   }
@@ -792,10 +899,8 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
     if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 2, S4>), grid, dim3(256), 0, st, g, 0);
     else hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1>), grid, dim3(256), 0, st, g, 0);
   }
-  if (splits > 1) {
-    const size_t n = (size_t)g.m * g.n;
-    hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, st, g, splits);
-  }
+  if (splits > 1)
+    hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3(reduce_blocks<EPI>(g.m, g.n)), dim3(256), 0, st, g, splits);
   return hipGetLastError();
 }
 
@@ -865,7 +970,8 @@ bool gemm_q_ok(int ak, int bk, int epi, int m, int n, int k) {
   if (n % 64) return false;
   if (ak == AK_I8)
     return bk == BK_I8 && (epi == EPI_SWIGLU_F32 || epi == EPI_STORE_F16 || epi == EPI_STORE_F32 || epi == EPI_STORE_I32);
-  return bk != BK_I8 && epi != EPI_STORE_I32 && epi != EPI_SWIGLU_F32;
+  if (ak == AK_F8X2) return bk == BK_MXFP4 && (epi == EPI_SWIGLU_F8X2 || epi == EPI_STORE_F16 || epi == EPI_STORE_F32);
+  return bk != BK_I8 && epi != EPI_STORE_I32 && epi != EPI_SWIGLU_F32 && epi != EPI_SWIGLU_F8X2;
 }
 
 #define MXQ_EPIS(AK, BK)                                                                            \
@@ -899,6 +1005,14 @@ hipError_t launch_gemm_q(int ak, int bk, int epi, const QGemmArgs& g, hipStream_
       case EPI_STORE_F16: return launch_wn<AK_I8, BK_I8, EPI_STORE_F16>(g, s, st);
       case EPI_STORE_F32: return launch_wn<AK_I8, BK_I8, EPI_STORE_F32>(g, s, st);
       case EPI_STORE_I32: return launch_wn<AK_I8, BK_I8, EPI_STORE_I32>(g, s, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (ak == AK_F8X2) {  // MXFP4 weights only (gemm_q_ok)
+    switch (epi) {
+      case EPI_SWIGLU_F8X2: return launch_wn<AK_F8X2, BK_MXFP4, EPI_SWIGLU_F8X2>(g, s, st);
+      case EPI_STORE_F16: return launch_wn<AK_F8X2, BK_MXFP4, EPI_STORE_F16>(g, s, st);
+      case EPI_STORE_F32: return launch_wn<AK_F8X2, BK_MXFP4, EPI_STORE_F32>(g, s, st);
       default: return hipErrorInvalidValue;
     }
   }

@@ -45,7 +45,19 @@ enum AKind : int {
   AK_F16 = 0,      // f16 [M][K]
   AK_F32 = 1,      // f32 [M][K] (rounded to f16 for the MFMA)
   AK_I8 = 2,       // int8 [M][K] + f32 per-row (token) scale [M]
+  AK_F8X2 = 3,     // two FP8 E4M3 terms + E8M0 scales per 64 K (the F8X2 layout below)
 };
+
+// F8X2: an activation matrix [M][K] (K % 64 == 0) as two FP8 E4M3 terms,
+// v ~= t1 * 2^(e1-127) + t2 * 2^(e2-127), with one E8M0 pair (e1, e2) per
+// row and 64-K group.  data [M][K/64][2 terms][64 bytes]: within a term the
+// group's values sit in the order k 0-15, 32-47, 16-31, 48-63 (lane half h
+// of a v_mfma_scale 32x32x64 FP8 operand holds k [16h, 16h+16) and
+// [32+16h, 32+16h+16)); e8 [K/64][M] dwords, bytes 0 / 1 = e1 / e2.
+inline size_t f8x2_data_bytes(size_t m, size_t k) { return 2 * m * k; }
+inline size_t f8x2_e8_bytes(size_t m, size_t k) { return m * (k / 64) * 4; }
+// f16 [M][K] -> F8X2 (mx_codecs.hip)
+hipError_t launch_split_f8x2(const uint16_t* x, int m, int k, uint8_t* data, uint32_t* e8, hipStream_t st);
 
 // Epilogues.
 enum Epi : int {
@@ -55,6 +67,7 @@ enum Epi : int {
   EPI_SWIGLU_HALF = 3,   // dual B: mid f16 = silu(clamp(g/16)) * u/16  (swiglu_half)
   EPI_SWIGLU_F32 = 4,    // dual B: mid f32 = silu(g) * u               (W8A8 mid)
   EPI_STORE_I32 = 5,     // C i32 [M][N], raw integer sums (AK_I8 x BK_I8, no scales)
+  EPI_SWIGLU_F8X2 = 6,   // dual B: mid = silu(g) * u in f32, stored as F8X2 (c data, c_e8 scales)
 };
 
 struct GemmArgs {
@@ -86,6 +99,8 @@ struct QGemmArgs {
   void* ws;                               // split-K partials (gemm_q_ws_bytes)
   int m, n, k;                            // n = rows of each weight matrix
   int tiles_m;                            // set by the launcher
+  const uint32_t* a_e8;                   // AK_F8X2: E8M0 pairs [K/64][M]
+  uint32_t* c_e8;                         // EPI_SWIGLU_F8X2: mid E8M0 pairs [N/64][M]
 };
 bool gemm_q_ok(int akind, int bkind, int epi, int m, int n, int k);
 size_t gemm_q_ws_bytes(int akind, int bkind, int epi, int m, int n, int k);

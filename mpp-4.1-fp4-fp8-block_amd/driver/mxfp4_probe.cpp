@@ -266,6 +266,7 @@ void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long i
         {MX_MLP_FUSED, "MXFP4 fused (plain SwiGLU, fp16 out): h_mxfp4_h", true},
         {MX_MLP_DEQUANT, "MXFP4 dequant (v_cvt_scalef32_pk_f16_fp4 -> half) + h_h_f", true},
         {MX_MLP_W4A4, "MXFP4 W4A4 (x, mid -> MXFP4; FP4 x FP4 scaled MFMA): fp4_fp4_h", true},
+        {MX_MLP_SCALED, "MXFP4 scaled MFMA (x, mid -> two E4M3 terms; FP8 x FP4 scaled MFMA): h_mxfp4_h", true},
     };
     for (const Variant& v : variants) {
       if (v.id == MX_MLP_W4A4 && (H % 128 || I % 128)) {

@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libmxfp4hip.so")
 MX_OK, MX_EINVAL, MX_ENODEV, MX_ENOKERNEL, MX_ENOMEM, MX_EGPU = range(6)
 DT_F32, DT_F16, DT_I8, DT_I32, DT_U8 = range(5)
 FMT_FP4_E2M1, FMT_FP8_E4M3, FMT_FP8_E5M2 = range(3)
-MLP_FUSED, MLP_DEQUANT, MLP_W4A4, MLP_REFROW = range(4)
+MLP_FUSED, MLP_DEQUANT, MLP_W4A4, MLP_REFROW, MLP_SCALED = range(5)
 PROBE_F16, PROBE_FP4, PROBE_FP8, PROBE_INT4, PROBE_I8 = range(5)
 WFMT_FP8_E4M3, WFMT_FP8_E5M2, WFMT_INT8, WFMT_INT4, WFMT_W8A8 = 1, 2, 3, 4, 5
 

@@ -53,7 +53,7 @@ def test_driver_mlp_benchmark_on_gpu():
     m = re.search(r"reference epilogue\): h_mxfp4_f:\n.*\n\s+checksum: ([-0-9.e+]+) over 32 samples", out)
     assert m, out
     assert abs(float(m.group(1)) - 403573) / 403573 < 2e-5
-    for row in ("W4A4", "FP8 E5M2 weights", "INT4 weights", "W8A8 MLP", "relative slowdown"):
+    for row in ("W4A4", "scaled MFMA", "FP8 E5M2 weights", "INT4 weights", "W8A8 MLP", "relative slowdown"):
         assert row in out
 
 
