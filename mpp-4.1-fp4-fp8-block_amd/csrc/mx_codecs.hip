@@ -463,26 +463,35 @@ hipError_t launch_fill_normal(void* dst, int dtype, size_t n, uint64_t seed, flo
 }
 
 // f16 [M][K] -> F8X2 (layout in mx_internal.h, split rule at
-// f8x2_split_store): 16 lanes per (row, 64-K group), 4 values per lane; a
-// group past the end exits as a whole.  (A lane pair per group with 64
-// contiguous bytes per lane measured slower: 7.6 against 6.0 us at T = 512,
-// K = 7168.)
+// f8x2_split_store): 4 lanes per (row, 64-K group), 16 values (two 16-byte
+// loads) per lane; a group past the end exits as a whole.  Measured at
+// T = 512, K = 7168 (split kernel alone, back to back): 2 lanes per group
+// 7.6 us, 4 lanes 4.3 us, 8 lanes 4.8 us, 16 lanes 6.2 us.
 __global__ void k_split_f8x2(const uint16_t* x, int m, int k, uint8_t* data, uint32_t* e8) {
   const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int j = (int)(t & 15);
+  const int j = (int)(t & 3);
   const int groups = k / 64;
-  const size_t gi = t >> 4;
+  const size_t gi = t >> 2;
   if (gi >= (size_t)m * groups) return;
   const int row = (int)(gi / groups), grp = (int)(gi % groups);
-  const uint2 w = *reinterpret_cast<const uint2*>(x + (size_t)row * k + (size_t)grp * 64 + 4 * j);
-  const float v[4] = {f16_bits_to_f32((uint16_t)(w.x & 0xffffu)), f16_bits_to_f32((uint16_t)(w.x >> 16)),
-                      f16_bits_to_f32((uint16_t)(w.y & 0xffffu)), f16_bits_to_f32((uint16_t)(w.y >> 16))};
-  f8x2_split_store<16>(v, j, data + (size_t)row * 2 * k + (size_t)grp * 128, e8 + (size_t)grp * m + row);
+  const uint16_t* src = x + (size_t)row * k + (size_t)grp * 64 + 16 * j;
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * q);
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[8 * q + 2 * e] = f16_bits_to_f32((uint16_t)(d[e] & 0xffffu));
+      v[8 * q + 2 * e + 1] = f16_bits_to_f32((uint16_t)(d[e] >> 16));
+    }
+  }
+  f8x2_split_store<4>(v, j, data + (size_t)row * 2 * k + (size_t)grp * 128, e8 + (size_t)grp * m + row);
 }
 
 hipError_t launch_split_f8x2(const uint16_t* x, int m, int k, uint8_t* data, uint32_t* e8, hipStream_t st) {
   if (m <= 0 || k <= 0 || k % 64) return hipErrorInvalidValue;
-  const size_t threads = (size_t)m * (k / 64) * 16;
+  const size_t threads = (size_t)m * (k / 64) * 4;
   hipLaunchKernelGGL(k_split_f8x2, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, x, m, k, data, e8);
   return hipGetLastError();
 }
