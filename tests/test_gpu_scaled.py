@@ -67,6 +67,16 @@ def test_config2_scaled(dev):
     d.free()
 
 
+def test_scaled_scales_from_global(dev):
+    """Gate/up with 192 tiles and no K split over K = 8192 (128 stages): the
+    workgroup's weight scales do not fit its LDS copy, so each stage loads
+    them from global memory next to the F8X2 scale pairs."""
+    d = MlpData(dev, 1536, 8192, 1024, seed=23)
+    rows = sample_rows(1536, 16)
+    check(run(dev, d, M.MLP_SCALED)[rows], oracle(d, rows=rows), "scaled, global scales")
+    d.free()
+
+
 def test_scaled_rejects_bad_shapes(dev):
     d = MlpData(dev, 4, 256, 512, seed=3)
     out = dev.alloc(4 * 256 * 2)
