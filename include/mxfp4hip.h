@@ -55,7 +55,9 @@ enum {
    * counterpart of the native scale-plane rows (MXFP4Kernels.metal:138-173). */
   MX_MLP_FUSED = 0,
   /* dequant: 3 x dequant-to-half, h_h_f gate/up, swiglu_float, down
-   * (encodeMXFP4DequantMLP main.swift:2426-2538). */
+   * (encodeMXFP4DequantMLP main.swift:2426-2538).  The down GEMM rounds the
+   * f32 mid to f16 for the fp16 MFMA, where the reference's f_h_f multiplies
+   * f32 x half (about 3e-3 of rms). */
   MX_MLP_DEQUANT = 1,
   /* W4A4: x and mid quantized to MXFP4 along K, FP4 x FP4 scaled MFMA
    * (v_mfma_scale_f32_32x32x64_f8f6f4), fp16 out. */
