@@ -190,7 +190,7 @@ constexpr int out_bytes(int epi) {
 // while one is computed, small enough for two workgroups per CU.  4: three
 // stages in flight, for launches of at most one workgroup per CU, which
 // otherwise sit in the DMA latency of every stage (8-bit / f16 weights,
-// BCH = 1 only).
+// and MXFP4 with its scales in LDS; BCH = 1 only).
 // SCL (4-bit weights): the E8M0 / f16 scales of the workgroup's weight rows
 // over its whole K range are copied into LDS before the loop (at most
 // kScLds bytes) and read from there per stage.  Loaded per stage from global
@@ -198,8 +198,11 @@ constexpr int out_bytes(int epi) {
 // latency the short stages do not cover.
 constexpr int kScLds = 16384;
 // F8X2 activations give 2 KB of it to the A slots' scale pairs, so that two
-// workgroups still share a CU (80 KB each).
-constexpr int sc_lds_bytes(int ak) { return ak == AK_F8X2 ? kScLds - 2048 : kScLds; }
+// workgroups still share a CU (80 KB each).  Beside the deep ring (one
+// workgroup per CU, 80 KB of slots) the copy may take 48 KB.
+constexpr int sc_lds_bytes(int ak, int ns = 2) {
+  return ns == 4 ? 49152 : ak == AK_F8X2 ? kScLds - 2048 : kScLds;
+}
 template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2, bool SCL = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
@@ -231,7 +234,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   constexpr int KSTEPS = 4;
   static_assert(NA >= 1 && (NBC >= 4 ? NBC % 4 == 0 : true), "tile / stage mismatch");
   static_assert(BCH == 1 || RBC == 128, "B chunks are whole 128-byte lines");
-  static_assert(NS == 2 || (NS == 4 && BCH == 1 && !SCALES4 && !GROUPED), "deep ring: per-stage B, no scales");
+  static_assert(NS == 2 || (NS == 4 && BCH == 1 && (!SCALES4 || SCL) && !GROUPED),
+                "deep ring: per-stage B, 4-bit scales from LDS");
   using AccT = typename std::conditional<AK == AK_I8, v16i, v16f>::type;
 
   // One __shared__ array per slot: the compiler then knows that a DMA into
@@ -242,7 +246,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // 128 tile rows (512 B) and a spare 512 B that waves 2 and 3 fill with
   // the same dwords, so that every wave issues the same loads per stage.
   constexpr int SA = NS == 2 ? kTM * RA + (AK == AK_F8X2 ? 1024 : 0) : 16, SB = NS == 2 ? TBR * RBC : 16;
-  constexpr int SD = NS > 2 ? kTM * RA + TBR * RBC : 16;
+  constexpr int SD = NS > 2 ? kTM * RA + TBR * RBC + (AK == AK_F8X2 ? 1024 : 0) : 16;
+  // F8X2 scale pairs of a stage: after A in the 2-slot A slot, after B in a deep slot
+  constexpr int ASC = NS == 2 ? kTM * RA : kTM * RA + TBR * RBC;
   __shared__ __attribute__((aligned(16))) uint8_t a_s0[SA];
   __shared__ __attribute__((aligned(16))) uint8_t a_s1[SA];
   __shared__ __attribute__((aligned(16))) uint8_t b_s0[SB];
@@ -262,8 +268,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   const int KT = K / KS / (int)gridDim.y;     // stages of this split
   const int kt0 = (int)blockIdx.y * KT;
   const size_t a_row = (size_t)K * (AK == AK_F32 ? 4 : (AK == AK_F16 || AK == AK_F8X2) ? 2 : 1);
-  static_assert(AK != AK_F8X2 || (BK == BK_MXFP4 && NS == 2 && !GROUPED),
-                "F8X2 activations: MXFP4 weights on the scaled MFMA, 2-slot ring");
+  static_assert(AK != AK_F8X2 || (BK == BK_MXFP4 && !GROUPED), "F8X2 activations: MXFP4 weights on the scaled MFMA");
   const size_t b_row = (size_t)b_row_bytes<BK>(K);
 
   // ---- DMA sources (per lane, per instruction)
@@ -324,12 +329,11 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
 
   uint32_t scv[2][NWB];  // 4-bit scales of the stage in flight / in use
-  uint32_t asv[2] = {0u, 0u};  // F8X2: E8M0 pair of A blocks 0 / 1 for the stage in use
 
   // SCL: the scale block [TBR rows][KT * KS/32 entries] into LDS, 2 bytes at a
   // time (rows and entries are 2-byte aligned), before any DMA is issued.
   constexpr int ESZ = BK == BK_INT4G32 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? sc_lds_bytes(AK) : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? sc_lds_bytes(AK, NS) : 16];
   const int sc_row = KT * (KS / 32) * ESZ;  // bytes of one row's scales
   if constexpr (SCL) {
     static_assert(SCALES4, "scales in LDS are for 4-bit weights");
@@ -351,7 +355,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     const size_t ka_ = (size_t)(kt0 + (S)) * RA;                                                   \
     _Pragma("unroll") for (int q = 0; q < NA; q++)                                                 \
       dma16(a_src[q] + ka_, (AS) + (wave * NA + q) * 1024);                                         \
-    if constexpr (AK == AK_F8X2) dma4(ae_src + (size_t)(kt0 + (S)) * M, (AS) + kTM * RA + wave * 256); \
+    if constexpr (AK == AK_F8X2) dma4(ae_src + (size_t)(kt0 + (S)) * M, (AS) + ASC + wave * 256);  \
   }
 #define MXQ_SCALES(S, P)                                                                           \
   {                                                                                                \
@@ -398,7 +402,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     _Pragma("unroll") for (int s = 0; s < KSTEPS; s++) {                                           \
       _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
         const int r_ = wm * 64 + i * 32 + r32;                                                     \
-        if (AK == AK_F8X2 && s == 0) asv[i] = *reinterpret_cast<const uint32_t*>((AS) + kTM * RA + r_ * 4); \
+        if (AK == AK_F8X2 && s == 0) AR##_sc[i] = *reinterpret_cast<const uint32_t*>((AS) + ASC + r_ * 4); \
         _Pragma("unroll") for (int w = 0; w < AW; w++) {                                           \
           /* F8X2: s = 2 * term + u, lane half h holds chunks 2h, 2h + 1 of each term */            \
           const int ch_ = AK == AK_F32 ? 8 * h + 2 * s + w : AK == AK_F8X2 ? 4 * (s >> 1) + 2 * h + (s & 1) : 4 * h + s; \
@@ -437,9 +441,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
         v8i b_;                                                                                    \
         _Pragma("unroll") for (int t = 0; t < 4; t++) { b_[t] = BR[0][j][t]; b_[4 + t] = 0; }      \
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a1_, b_, (v16f)acc[i][j], 0, 4, 0, \
-                                                                    (int)asv[i], 0, (int)scv[P][j]); \
+                                                                    (int)AR##_sc[i], 0, (int)scv[P][j]); \
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a2_, b_, (v16f)acc[i][j], 0, 4, 1, \
-                                                                    (int)asv[i], 0, (int)scv[P][j]); \
+                                                                    (int)AR##_sc[i], 0, (int)scv[P][j]); \
       }                                                                                            \
     }                                                                                              \
   }
@@ -504,6 +508,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 #define MXQ_COMPUTE(AS, BS, P, POS)                                                                \
   {                                                                                                \
     v4i ar_[KSTEPS][2][AW];                                                                        \
+    uint32_t ar__sc[2] = {0u, 0u}; /* F8X2: E8M0 pairs of A blocks 0 / 1 */                       \
     v4i br_[BREADS][NWB];                                                                          \
     MXQ_READ(AS, BS, (POS) * (RB / 16), ar_, br_)                                                  \
     __builtin_amdgcn_sched_barrier(0); /* keep the reads ahead of the MFMAs */                     \
@@ -563,6 +568,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 #define MXQ_DEEP(U, CUR, NXT)                                                                      \
   {                                                                                                \
     const int st_ = kt + (U);                                                                      \
+    constexpr int PC_ = (U) & 1; /* scale set of stage st (4-bit weights) */                       \
     /* the previous stage's MFMAs stay ahead of this wait: moved past it, they */                  \
     /* would leave the next stage's LDS reads nothing to overlap */                                \
     __builtin_amdgcn_sched_barrier(0);                                                             \
@@ -573,12 +579,14 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     MXQ_DMA_A(min(st_ + NS, KT - 1), MXQ_AS(U))                                                    \
     MXQ_DMA_B(min(st_ + NS, KT - 1), MXQ_BS(U))                                                    \
     MXQ_READ(MXQ_AS(((U) + 1) % NS), MXQ_BS(((U) + 1) % NS), 0, NXT##_a, NXT##_b)                  \
+    if constexpr (SCALES4) MXQ_SCALES(min(st_ + 1, KT - 1), PC_ ^ 1)                               \
     __builtin_amdgcn_sched_barrier(0);                                                             \
-    MXQ_MATH(CUR##_a, CUR##_b, 0)                                                                  \
+    MXQ_MATH(CUR##_a, CUR##_b, PC_)                                                                \
   }
   if constexpr (NS > 2) {
     static_assert(NS == 4 && (NS - 1) * (VM_A + NB) <= 63, "vmcnt range");
     v4i f0_a[KSTEPS][2][AW], f1_a[KSTEPS][2][AW];
+    uint32_t f0_a_sc[2] = {0u, 0u}, f1_a_sc[2] = {0u, 0u};  // F8X2: E8M0 pairs by fragment set
     v4i f0_b[BREADS][NWB], f1_b[BREADS][NWB];
     MXQ_DMA_A(0, MXQ_AS(0)) MXQ_DMA_B(0, MXQ_BS(0))
     MXQ_DMA_A(1, MXQ_AS(1)) MXQ_DMA_B(1, MXQ_BS(1))
@@ -589,6 +597,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     MXQ_READ(MXQ_AS(0), MXQ_BS(0), 0, f0_a, f0_b)
+    if constexpr (SCALES4) MXQ_SCALES(0, 0)
     __builtin_amdgcn_sched_barrier(0);
     for (int kt = 0; kt < KT; kt += NS) {
       MXQ_DEEP(0, f0, f1) MXQ_DEEP(1, f1, f0) MXQ_DEEP(2, f0, f1) MXQ_DEEP(3, f1, f0)
@@ -680,12 +689,16 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   if constexpr (EPI == EPI_SWIGLU_F8X2) {
     // mid = silu(g) * u of the tile's 128 rows x 64 channels, which is one
     // 64-K group of the down GEMM's F8X2 input, goes through LDS: wave
-    // (wm, wn) writes rows [64 wm, +64) x channels [32 wn, +32) into A slot
-    // wm (row r, channel c at r * 64 + (c ^ (r & 31)): the column writes and
-    // the row reads both spread over the banks), then lane pair p of the
+    // (wm, wn) writes rows [64 wm, +64) x channels [32 wn, +32) into ring
+    // slot wm (16 KB each: the 2-slot A slots or the first two deep slots;
+    // row r, channel c at r * 64 + (c ^ (r & 31)): the column writes and the
+    // row reads both spread over the banks), then lane pair p of the
     // workgroup splits row p.
+    static_assert((NS == 2 ? SA : SD) >= 64 * 64 * 4, "mid tile half fits a ring slot");
+    uint8_t* const ms0 = NS == 2 ? a_s0 : d_s0;
+    uint8_t* const ms1 = NS == 2 ? a_s1 : d_s1;
     __syncthreads();
-    float* ml = reinterpret_cast<float*>(wm ? a_s1 : a_s0);
+    float* ml = reinterpret_cast<float*>(wm ? ms1 : ms0);
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -696,7 +709,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       }
     __syncthreads();
     const int pr = tid >> 1, half = tid & 1, rl = pr & 63;
-    const float* src = reinterpret_cast<const float*>(pr < 64 ? a_s0 : a_s1);
+    const float* src = reinterpret_cast<const float*>(pr < 64 ? ms0 : ms1);
     float mv[32];
 #pragma unroll
     for (int k = 0; k < 32; k++) {
@@ -846,19 +859,23 @@ template <int AK, int BK> constexpr int b_chunk() {
 }
 
 // True when a workgroup's scales over kt stages fit the LDS copy (SCL).
-template <int AK, int BK, int NWB> bool sc_lds_fits(int kt) {
-  return NWB * 64 * kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1) <= sc_lds_bytes(AK);
+template <int AK, int BK, int NWB, int NS = 2> bool sc_lds_fits(int kt) {
+  return NWB * 64 * kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1) <= sc_lds_bytes(AK, NS);
 }
 
 // Launches of at most this many workgroups (one per CU) take the deep ring,
 // for weight formats staged per stage whose four slots fit the 160 KB of LDS
-// (not f32 activations x f16 weights: 4 x 48 KB).
+// (not f32 activations x f16 weights: 4 x 48 KB).  MXFP4 weights under f16
+// activations take it too, with their E8M0 scales in LDS beside the ring
+// (80 KB + up to 48 KB) when those fit, for splits of at least 16 stages
+// (C2's down GEMM, 224 workgroups: 27.4 -> 24.4 us).
 constexpr int kDeepMaxWgs = 256;
 constexpr bool deep_format(int ak, int bk) {
   const int ks = ak == AK_I8 ? 128 : 64;
   const int ra = ak == AK_F32 ? 256 : 128;
   const int rb = bk == BK_F16 ? ks * 2 : ks;
-  return bk != BK_MXFP4 && bk != BK_INT4G32 && 4 * 128 * (ra + rb) <= 160 * 1024;
+  if (bk == BK_MXFP4) return ak == AK_F16 || ak == AK_F8X2;
+  return bk != BK_INT4G32 && 4 * 128 * (ra + rb) <= 160 * 1024;
 }
 
 // Workgroups of the split-K reduction: 4 outputs per thread (16 lanes per
@@ -880,9 +897,14 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   // chunked B once a split spans at least four chunks (a shorter split would
   // wait for its whole B up front)
   if constexpr (deep_format(AK, BK)) {
-    if (g.tiles_m * tiles_n * splits <= kDeepMaxWgs && kt >= 8 && kt % 4 == 0) {
-      hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 4>), dim3(g.tiles_m * tiles_n, splits), dim3(256), 0,
-                         st, g, 0);
+    // MXFP4: scales in LDS, and at least 16 stages (C0's 8-stage splits
+    // measured 1 us slower per GEMM on the deep ring: its fill and drain
+    // are not repaid)
+    constexpr bool S4D = BK == BK_MXFP4;
+    if (g.tiles_m * tiles_n * splits <= kDeepMaxWgs && kt >= 8 && kt % 4 == 0 &&
+        (!S4D || (kt >= 16 && sc_lds_fits<AK, BK, NWB, 4>(kt)))) {
+      hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 4, S4D>), dim3(g.tiles_m * tiles_n, splits), dim3(256),
+                         0, st, g, 0);
       if (splits > 1)
         hipLaunchKernelGGL((k_gemm_q_reduce<AK, BK, EPI>), dim3(reduce_blocks<EPI>(g.m, g.n)), dim3(256), 0, st, g,
                            splits);
@@ -953,7 +975,10 @@ int gemm_q_splits(int ak, int bk, int epi, int m, int n, int k) {
   int s = 1;
   if (deep_format(ak, bk) && kt % 4 == 0) {
     while (tiles * 2 * s <= kDeepMaxWgs && kt % (8 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
-    if (tiles * s >= 192) return s;  // else too few workgroups: the 2-slot policy below
+    const int nwb = is_dual(epi) || n % 128 == 0 ? 2 : 1;
+    // else too few workgroups, or MXFP4 scales too large for LDS: the 2-slot policy below
+    if (tiles * s >= 192 && (bk != BK_MXFP4 || (kt / s >= 16 && nwb * 64 * (kt / s) * 2 <= sc_lds_bytes(ak, 4))))
+      return s;
     s = 1;
   }
   while (tiles * s < 384 && kt % (2 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
