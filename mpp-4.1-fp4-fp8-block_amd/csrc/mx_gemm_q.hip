@@ -973,12 +973,11 @@ int gemm_q_splits(int ak, int bk, int epi, int m, int n, int k) {
   const int kt = k / stage_k(ak);
   if (tiles >= 192) return 1;
   int s = 1;
-  if (deep_format(ak, bk) && kt % 4 == 0) {
+  // (MXFP4 keeps the 2-slot split policy: C2's gate/up GEMM as 2 deep splits
+  // of 56 stages measured 2-3 us slower than 4 two-slot splits of 28)
+  if (deep_format(ak, bk) && bk != BK_MXFP4 && kt % 4 == 0) {
     while (tiles * 2 * s <= kDeepMaxWgs && kt % (8 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
-    const int nwb = is_dual(epi) || n % 128 == 0 ? 2 : 1;
-    // else too few workgroups, or MXFP4 scales too large for LDS: the 2-slot policy below
-    if (tiles * s >= 192 && (bk != BK_MXFP4 || (kt / s >= 16 && nwb * 64 * (kt / s) * 2 <= sc_lds_bytes(ak, 4))))
-      return s;
+    if (tiles * s >= 192) return s;  // else too few workgroups: the 2-slot policy below
     s = 1;
   }
   while (tiles * s < 384 && kt % (2 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
