@@ -16,7 +16,9 @@
 //               E8M0 block), decodes them with v_cvt_scalef32_pk_f16_fp4 and
 //               feeds v_mfma_f32_16x16x32_f16 (tokens padded to 16 rows; the
 //               MFMA is never the bottleneck).  The activations follow the
-//               same K permutation.
+//               same K permutation.  In the whole-line layout the loads move
+//               two steps of 8 rows (one 128-byte line each) and the lanes
+//               swap halves with a DPP rotate to get the same operands.
 //   order     = the activations (LDS DMA) and the rows' E8M0 scales are
 //               requested first, then every weight load of the wave
 //               (scheduling barriers keep the order).  vmcnt retires in
@@ -65,7 +67,10 @@ __host__ __device__ inline size_t gemv_lds_bytes(int t, int k, int ng = 1) {
 // K; WPG waves share each group's K steps.  More groups per workgroup stage
 // x once for more rows (the activations are T x K, as large as 16 rows of
 // weights at T = 4).
-template <bool DUAL, int NSTEP, int WPG>
+// WL picks the weight load layout.  Whole lines (WL): one load moves one
+// 128-byte line (two K steps) of 8 rows.  Half lines: one load moves one K
+// step (64 bytes) of all 16 rows.
+template <bool DUAL, int NSTEP, int WPG, bool WL>
 __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* lds) {
   constexpr int NG = kW / WPG;
   static_assert(NG * WPG == kW && NG <= 8, "row groups per workgroup");
@@ -97,6 +102,25 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   const uint8_t* srow;
   row_ptrs(gi * 16 + r, wrow, srow);
   wrow += lg * 16;
+  // Whole-line loads.  K line column c (256 K = one 128-byte line per row)
+  // holds steps 2c and 2c+1.  Load A moves rows 0-7 of the group, load B rows
+  // 8-15: 8 whole lines per instruction, against 16 half lines when each load
+  // is one step of all 16 rows (measured, weights alone at C1 gate/up: 3.5
+  // against 4.5 us).  Lane (r, lg) takes 16 bytes of step 2c of its own row
+  // from the load holding that row, and 16 bytes of step 2c+1 of row r ^ 8
+  // from the other load, so that step 2c is a per-lane select of A / B and
+  // step 2c+1 is the other select rotated by 8 lanes (DPP row_ror:8).
+  const uint8_t* wA;
+  const uint8_t* wB;
+  const uint8_t* s_unused;
+  row_ptrs(gi * 16 + (r & 7), wA, s_unused);
+  row_ptrs(gi * 16 + 8 + (r & 7), wB, s_unused);
+  wA += lg * 16;
+  wB += lg * 16;
+  const int hiA = r >= 8 ? 64 : 0, hiB = r < 8 ? 64 : 0;  // A / B lanes holding step 2c+1
+  const int LC = (S + 1) / 2;                               // line columns (the last may be half)
+  constexpr int NLC = NSTEP / 2;                            // line columns per batch
+  static_assert(NSTEP % 2 == 0, "line columns load in pairs");
 
   // 1) Staging first: x rows go global -> LDS by DMA (no registers), the 16
   //    rows' scales into a few registers.  Issued before the weight loads,
@@ -125,15 +149,34 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2) This wave's first batch of weight loads.
+  // 2) This wave's first batch of weight loads: line columns gw + i WPG,
+  //    A then B.  Tail columns re-read the last valid one; in a half column
+  //    (odd S) the lanes of step 2c+1 re-read step 2c.
   uint4 wv[NSTEP];
+  auto load_batch = [&](int p0) {
+    if constexpr (WL) {
 #pragma unroll
-  for (int b = 0; b < NSTEP; b++) {
-    const int st = min(gw + b * WPG, S - 1);  // tail steps re-read a valid step
-    const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
-    wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+      for (int i = 0; i < NLC; i++) {
+        const int c = min(p0 + i * WPG, LC - 1);
+        const bool two = 2 * c + 1 < S;
+        const v4i a4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wA + (size_t)c * 128 + (two ? hiA : 0)));
+        wv[2 * i] = make_uint4(a4[0], a4[1], a4[2], a4[3]);
+        __builtin_amdgcn_sched_barrier(0);
+        const v4i b4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wB + (size_t)c * 128 + (two ? hiB : 0)));
+        wv[2 * i + 1] = make_uint4(b4[0], b4[1], b4[2], b4[3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {  // steps p0 + b WPG; tail steps re-read a valid step
+#pragma unroll
+      for (int b = 0; b < NSTEP; b++) {
+        const int st = min(p0 + b * WPG, S - 1);
+        const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
+        wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  load_batch(gw);
 
   // 3) Staging landed (only the NSTEP weight loads may still be in flight):
   //    scales to LDS, then a bare barrier (__syncthreads would also wait for
@@ -188,39 +231,47 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
       }
     }
   } else {
-    for (int s0 = gw; s0 < S; s0 += WPG * NSTEP) {
-      if (s0 != gw) {  // later batches (more than NSTEP steps per wave): load them now
-#pragma unroll
-        for (int b = 0; b < NSTEP; b++) {
-          const int st = min(s0 + b * WPG, S - 1);
-          const v4i w4 = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + (size_t)st * 64));
-          wv[b] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-      // LDS operands are read one step ahead of their MFMAs so that LDS
-      // latency overlaps the previous step's decode and MFMAs.
+    // Batch positions p0 count line columns (whole lines) or steps.
+    constexpr int PER = WL ? NLC : NSTEP;
+    const int P = WL ? LC : S;
+    for (int p0 = gw; p0 < P; p0 += WPG * PER) {
+      if (p0 != gw) load_batch(p0);  // later batches (more than one per wave)
+      // Steps of the batch in order (whole lines: 2c, 2c+1 per column).  LDS
+      // operands are read one step ahead of their MFMAs so that LDS latency
+      // overlaps the previous step's decode and MFMAs.
+      auto step_of = [&](int k) { return WL ? 2 * (p0 + (k >> 1) * WPG) + (k & 1) : p0 + k * WPG; };
       uint4 xn[4];
       uint32_t sn;
       {
-        const int st = min(s0, S - 1);
+        const int st = min(step_of(0), S - 1);
 #pragma unroll
         for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)st * kStepK + q * 8);
         sn = sr[(size_t)st * 4];
       }
 #pragma unroll
-      for (int b = 0; b < NSTEP; b++) {
-        const int st = s0 + b * WPG;
+      for (int k = 0; k < NSTEP; k++) {
+        const int st = step_of(k);
         uint4 xq[4] = {xn[0], xn[1], xn[2], xn[3]};
         const uint32_t sbyte = sn;
-        if (b + 1 < NSTEP) {
-          const int stn = min(st + WPG, S - 1);
+        if (k + 1 < NSTEP) {
+          const int stn = min(step_of(k + 1), S - 1);
 #pragma unroll
           for (int q = 0; q < 4; q++) xn[q] = *reinterpret_cast<const uint4*>(xr + (size_t)stn * kStepK + q * 8);
           sn = sr[(size_t)stn * 4];
         }
         if (st < S) {  // wave-uniform; no global loads inside
-          const uint32_t wd[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
+          const uint4 a = wv[k & ~1], b = wv[k | 1];
+          uint32_t wd[4];
+          if (!WL) {
+            wd[0] = wv[k].x; wd[1] = wv[k].y; wd[2] = wv[k].z; wd[3] = wv[k].w;
+          } else if ((k & 1) == 0) {  // step 2c: the lane's own row, from A (rows 0-7) or B
+            wd[0] = r < 8 ? a.x : b.x; wd[1] = r < 8 ? a.y : b.y;
+            wd[2] = r < 8 ? a.z : b.z; wd[3] = r < 8 ? a.w : b.w;
+          } else {  // step 2c+1: held 8 lanes away, in the other load
+            const uint32_t o[4] = {r < 8 ? b.x : a.x, r < 8 ? b.y : a.y, r < 8 ? b.z : a.z, r < 8 ? b.w : a.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) wd[q] = (uint32_t)__builtin_amdgcn_mov_dpp((int)o[q], 0x128, 0xf, 0xf, false);
+          }
           const float scale = e8m0_as_cvt_scale(sbyte);
 #pragma unroll
           for (int q = 0; q < 4; q++)
@@ -251,15 +302,22 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   }
 }
 
+// One launch per MLP half: whole lines for the dual gate/up pass, half lines
+// for down (measured at C1, T = 1 / T = 8, down: 4.42 / 5.22 us with whole
+// lines against 4.32 / 5.08 us; gate/up gains 0.15-0.2 us from them).
 template <bool DUAL, int NSTEP, int WPG>
 __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  gemv_body<DUAL, NSTEP, WPG>(g, blockIdx.x * (kW / WPG), lds);
+  gemv_body<DUAL, NSTEP, WPG, DUAL>(g, blockIdx.x * (kW / WPG), lds);
 }
 
 // Grouped (MoE) form: blockIdx.y is the group (expert).  Group e owns token
 // rows [off[e], off[e+1]) of x and out, and its weights sit e * stride bytes
-// after group 0's.  Groups with no tokens exit at once.
+// after group 0's.  Groups with no tokens exit at once.  Whole-line loads
+// for both passes: these launches stream far more weights than one MLP and
+// are bandwidth-bound, where fewer, whole-line requests pay (measured at 64
+// experts x 4 tokens of the C1 shape: 360 -> 297 us per MoE MLP, down alone
+// 113 -> 105 us).
 template <bool DUAL, int NSTEP, int WPG>
 __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4_grouped(GemvArgs g, GroupTable gt) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -275,7 +333,7 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4_grouped(GemvArgs g, Grou
     g.b1 += e * gt.b_stride;
     g.s1 += e * gt.s_stride;
   }
-  gemv_body<DUAL, NSTEP, WPG>(g, blockIdx.x * (kW / WPG), lds);
+  gemv_body<DUAL, NSTEP, WPG, true>(g, blockIdx.x * (kW / WPG), lds);
 }
 
 template <bool DUAL, int NSTEP, int WPG>
