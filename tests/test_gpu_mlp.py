@@ -251,8 +251,11 @@ def test_benchmark_entry_point(dev):
 
 # ---- decode GEMV path (tokens <= 16) -----------------------------------------
 # Shapes: fewest workgroups (H = I = 128, down waves with no K step), several
-# load batches per wave (K = 8192 and 16384), the largest token count.
-@pytest.mark.parametrize("T,H,I", [(3, 128, 128), (4, 256, 8192), (1, 16384, 128), (16, 1024, 512)])
+# load batches per wave (K = 8192 and 16384), the largest token count, and
+# gate/up K with an odd number of 128-K steps under the rolling whole-line
+# issue (H = 4480 and 4224: a half last line column, tail columns clamped).
+@pytest.mark.parametrize("T,H,I", [(3, 128, 128), (4, 256, 8192), (1, 16384, 128), (16, 1024, 512),
+                                   (1, 4480, 384), (5, 4224, 640)])
 def test_decode_gemv_shapes(dev, T, H, I):
     d = MlpData(dev, T, H, I, seed=T + H // 128)
     check(run_mlp(dev, d, M.MLP_FUSED), oracle_mlp(d, M.MLP_FUSED), what=f"decode T={T} H={H} I={I}")

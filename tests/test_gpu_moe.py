@@ -81,6 +81,7 @@ def check(got, ref, what):
                                                                               # two row groups each
     ([i % 5 for i in range(64)], 1024, 512),  # >= 4096 one-group workgroups in both launches: four each
     ([i % 4 for i in range(128)], 1024, 256),  # down >= 8192: eight each; gate/up four
+    ([2, 0, 3, 1], 4480, 384),              # gate/up: rolling whole-line issue, odd step count
 ])
 def test_moe_decode_experts(dev, counts, H, I):
     d = MoeData(dev, counts, H, I, seed=len(counts) + H)
