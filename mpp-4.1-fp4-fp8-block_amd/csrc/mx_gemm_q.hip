@@ -972,6 +972,11 @@ int gemm_q_splits(int ak, int bk, int epi, int m, int n, int k) {
   const int tiles = ((m + kTM - 1) / kTM) * (is_dual(epi) ? n / 64 : (n % 128 == 0 ? n / 128 : n / 64));
   const int kt = k / stage_k(ak);
   if (tiles >= 192) return 1;
+  // MXFP4 gate/up with f16 activations and 16 stages: unsplit on the deep
+  // ring, the SwiGLU in the GEMM's epilogue, no reduce launch (C0's gate/up
+  // step 15.75 -> 15.0 us).  The F8X2 form measured slower that way (14.7
+  // -> 16.0 us) and keeps two splits.
+  if (bk == BK_MXFP4 && ak == AK_F16 && is_dual(epi) && kt <= 16 && tiles <= kDeepMaxWgs) return 1;
   int s = 1;
   // (MXFP4 keeps the 2-slot split policy: C2's gate/up GEMM as 2 deep splits
   // of 56 stages measured 2-3 us slower than 4 two-slot splits of 28)
