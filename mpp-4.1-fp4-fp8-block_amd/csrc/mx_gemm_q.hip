@@ -927,11 +927,15 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
 }
 
 // Plain (non-SwiGLU) GEMMs take 128-row weight tiles when N allows, except
-// MXFP4 with fewer than 16 of them: 64-row tiles then give the split-K grid
-// twice the tiles (C0's down GEMM, N = 1024: 13.5 -> 12.6 us per step with
-// its reduce; 12.25 -> 11.5 us on the F8X2 path).
+// MXFP4 with fewer than 16 of them and INT4 with fewer than 64: 64-row tiles
+// then give the grid twice the tiles (C0's down GEMM, N = 1024: 13.5 ->
+// 12.6 us per step with its reduce, 12.25 -> 11.5 us on the F8X2 path; C3
+// INT4's down GEMM, N = 4096: the MLP 96.8 -> 94.1 us in stream mode).
+// Other formats measured no gain (C3) or a loss (C2 dequant, f16 weights:
+// +2.5 us).
 inline bool wide_tiles(int bk, int epi, int n) {
-  return !is_dual(epi) && n % 128 == 0 && !(bk == BK_MXFP4 && n / 128 < 16);
+  return !is_dual(epi) && n % 128 == 0 && !(bk == BK_MXFP4 && n / 128 < 16) &&
+         !(bk == BK_INT4G32 && n / 128 < 64);
 }
 
 template <int AK, int BK, int EPI>
