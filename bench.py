@@ -10,6 +10,11 @@ down(silu(gate(x)) * up(x)).
 Secondary measurements (configs 0, 1 with T=8, 2, 3 and 4, and MoE grouped
 experts at the C1 and C2 expert shapes) are reported in
 the same JSON line under "secondary"; they are not the headline value.
+Each carries a "roofline" block for its longest GEMM/GEMV step (HBM for the
+decode GEMVs and the dequant kernels, the MFMA peak of the row's arithmetic
+otherwise: f16 for fp16-MFMA rows and for the scaled row, whose two FP8 x FP4
+MFMAs per block take the time of one f16 MFMA; FP4 for W4A4), or for the
+whole MLP where the library reports no per-step times (C3, MoE).
 
   value        effective TFLOP/s = 6*T*H*I / (time per step)
   roofline     the dominant kernel (fused gate/up GEMV): algorithmic bytes per
@@ -40,6 +45,47 @@ DEQUANT_NOTE = ("down GEMM rounds the f32 mid to f16 for the fp16 MFMA (the refe
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def roofline_block(bound, work, us, peak_key, kernel):
+    """{bound, achieved, peak, unit, frac} for `work` algorithmic bytes
+    (bound "hbm") or flops (bound "mfma") done in `us` microseconds."""
+    rate = work / (us * 1e-6)
+    if bound == "hbm":
+        return {"bound": "hbm", "achieved": round(rate / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(rate / HBM_PEAK, 4), "kernel": kernel, "kernel_us": round(us, 3)}
+    peak = PEAK[peak_key]
+    return {"bound": "mfma", "achieved": round(rate / 1e12, 1), "peak": peak / 1e12, "unit": "TFLOP/s",
+            "peak_dtype": peak_key, "frac": round(rate / peak, 4), "kernel": kernel, "kernel_us": round(us, 3)}
+
+
+def kernel_work(name, T, H, I):
+    """(bound, algorithmic flops or bytes) of one step kernel of an MLP row,
+    from its name in the library's kernel table."""
+    if name.startswith("gemv_"):  # decode GEMV: weights + activations in and out
+        if "gate_up" in name:
+            return "hbm", 2 * mxfp4_bytes(I, H) + T * H * 2 + T * I * 2
+        return "hbm", mxfp4_bytes(H, I) + T * I * 2 + T * H * 2
+    if name.startswith("dequant_"):  # MXFP4 in, f16 out
+        return "hbm", mxfp4_bytes(I, H) + I * H * 2
+    if "gate_up" in name:
+        return "mfma", 2 * T * H * 2 * I
+    if name.endswith("_gate") or name.endswith("_up") or name.endswith("_down") or "down" in name:
+        return "mfma", 2 * T * H * I
+    return None, 0
+
+
+def secondary_roofline(r, T, H, I, peak_key):
+    """Roofline of a secondary row's dominant (longest) GEMM/GEMV kernel."""
+    best = None
+    for name, us in (r.get("kernel_us") or {}).items():
+        bound, work = kernel_work(name, T, H, I)
+        if bound and (best is None or us > best[3]):
+            best = (name, bound, work, us)
+    if best is None:
+        return None
+    name, bound, work, us = best
+    return roofline_block(bound, work, us, peak_key, name)
 
 
 def mxfp4_bytes(n, k):
@@ -310,11 +356,13 @@ def main():
             r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2, cpu=cpu and 8)
             b = 3 * mxfp4_bytes(2048, 7168) + 2 * 8 * 7168 * 2
             r["hbm_frac"] = round(b / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
+            r["roofline"] = secondary_roofline(r, 8, 7168, 2048, "f16")
             sec["c1_t8_fused"] = r
         if want("c4"):
             r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, 1, 10, 2, seed=4,
                               cpu=cpu and 64)
             r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
+            r["roofline"] = secondary_roofline(r, 4096, 8192, 28672, "fp4")
             sec["c4_w4a4"] = r
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_W4A4, "w4a4"),
                        (M.MLP_SCALED, "scaled")):
@@ -324,6 +372,7 @@ def main():
                               cpu=cpu and tag == "fused" and 128)
             if v == M.MLP_DEQUANT:
                 r["note"] = DEQUANT_NOTE
+            r["roofline"] = secondary_roofline(r, 128, 1024, 4096, "fp4" if tag == "w4a4" else "f16")
             sec[f"c0_{tag}"] = r
         # the scaled row runs two FP8 x FP4 MFMAs per block (x split in two
         # E4M3 terms): the MFMA time of one f16 MFMA, so its useful FLOP/s are
@@ -336,6 +385,7 @@ def main():
             r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
             if v == M.MLP_DEQUANT:
                 r["note"] = DEQUANT_NOTE
+            r["roofline"] = secondary_roofline(r, 512, 7168, 2048, "f16")
             sec[f"c2_{tag}"] = r
         for wfmt, tag in ((M.WFMT_FP8_E4M3, "fp8_e4m3"), (M.WFMT_FP8_E5M2, "fp8_e5m2"),
                           (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32"), (M.WFMT_W8A8, "w8a8")):
@@ -348,14 +398,20 @@ def main():
             r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, n_sets, 40, 4, seed=7,
                               wfmt=wfmt, cpu=cpu and 128)
             r["hbm_frac"] = round(wb / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
+            # no per-kernel split for the format rows: the whole MLP's weight bytes
+            r["roofline"] = roofline_block("hbm", wb, r["us_per_iter"], None, "whole MLP (weights)")
             sec[f"c3_{tag}"] = r
         if want("moe"):
             # MoE grouped launches at the C1 / C2 expert shapes: 64 experts x 4
             # tokens (1.5 GB of expert weights per pass) and 8 experts x 512
-            sec["moe_c1_64x4"] = run_moe(dev, M, "MoE C1 shape 64 experts x 4 tokens", 64, 4, 7168, 2048,
-                                         40, 4, seed=8)
+            r = run_moe(dev, M, "MoE C1 shape 64 experts x 4 tokens", 64, 4, 7168, 2048, 40, 4, seed=8)
+            r["roofline"] = roofline_block("hbm", r["weight_bytes"] + 2 * 256 * 7168 * 2, r["us_per_iter"], None,
+                                           "whole MoE pass (two grouped launches)")
+            sec["moe_c1_64x4"] = r
             r = run_moe(dev, M, "MoE C2 shape 8 experts x 512 tokens", 8, 512, 7168, 2048, 20, 2, seed=9)
             r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
+            r["roofline"] = roofline_block("mfma", 6.0 * 4096 * 7168 * 2048, r["us_per_iter"], "f16",
+                                           "whole MoE pass (two grouped launches)")
             sec["moe_c2_8x512"] = r
         result["secondary"] = sec
 
