@@ -71,7 +71,7 @@ __host__ __device__ inline size_t gemv_lds_bytes(int t, int k, int ng = 1) {
 // WL picks the weight load layout.  Whole lines (WL): one load moves one
 // 128-byte line (two K steps) of 8 rows.  Half lines: one load moves one K
 // step (64 bytes) of all 16 rows.
-template <bool DUAL, int NSTEP, int WPG, bool WL>
+template <bool DUAL, int NSTEP, int WPG, bool WL, bool SC16>
 __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* lds) {
   constexpr int NG = kW / WPG;
   static_assert(NG * WPG == kW && NG <= 8, "row groups per workgroup");
@@ -136,23 +136,34 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
               reinterpret_cast<uint8_t*>(x_lds) + (size_t)t * (K + 8) * 2 + c * 1024);
     }
   }
-  const int n_sdw = 16 * NG * (KB / 4);  // scale dwords of the workgroup's rows
-  constexpr int SREGS = scale_regs(NG);
-  uint32_t sreg[SREGS];
+  // The rows' E8M0 bytes.  Passes wholly past them are skipped; inside the
+  // last pass, lanes past the end re-read the last piece (no predicated
+  // loads).  SC16 (the single launches): 16-byte pieces, each 8-row block
+  // (8 gate or 8 up channels, or 8 consecutive rows) being contiguous in
+  // memory and in LDS.  Otherwise (the grouped launches) dwords.  Measured:
+  // C1 T=1 gate/up 6.0 -> 5.68 us with pieces; the grouped launches at 64
+  // experts x 4 tokens went 199 -> 221 us (gate/up) and 97 -> 102 us
+  // (down) with pieces, so they keep dwords.  Skipping the passes past the
+  // scales took the C1 down pass from 4.27 to 3.94-3.99 us.
+  constexpr int SPAS = SC16 ? scale_regs(NG) / 4 : scale_regs(NG);  // passes of 64 kW pieces
+  const int QB = SC16 ? KB / 2 : 2 * KB;                             // pieces per 8-row block
+  const int n_sq = 2 * NG * QB;                                      // pieces of the workgroup's rows
+  constexpr int PW = SC16 ? 4 : 1;                                   // dwords per piece
+  uint32_t sreg[SPAS][PW];
 #pragma unroll
-  for (int q = 0; q < SREGS; q++) {
-    // Passes wholly past the rows' scales are skipped; inside the last pass,
-    // lanes past the end re-read the last dword (no predicated loads).
-    // Measured at C1 T=1 (down: 256 scale dwords for 2048 slots): down 4.27
-    // -> 3.94-3.99 us against clamping every slot (skipping by whole waves
-    // inside the pass measured 4.10 us).
-    if (q * 64 * kW >= n_sdw) break;
-    const int i = min(tid + q * 64 * kW, n_sdw - 1);
-    const int wr = i / (KB / 4), c = i % (KB / 4);
+  for (int q = 0; q < SPAS; q++) {
+    if (q * 64 * kW >= n_sq) break;
+    const int j = min(tid + q * 64 * kW, n_sq - 1);
+    const int b = j / QB, o = j % QB;
     const uint8_t* w;
     const uint8_t* s;
-    row_ptrs(wr, w, s);
-    sreg[q] = *reinterpret_cast<const uint32_t*>(s + c * 4);
+    row_ptrs(8 * b, w, s);
+    if constexpr (SC16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(s + o * 16);
+      sreg[q][0] = v.x; sreg[q][1] = v.y; sreg[q][2] = v.z; sreg[q][3] = v.w;
+    } else {
+      sreg[q][0] = *reinterpret_cast<const uint32_t*>(s + o * 4);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -205,11 +216,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   //    the weights).
   __builtin_amdgcn_s_waitcnt(gemv_wait_vm(INFL));
 #pragma unroll
-  for (int q = 0; q < SREGS; q++) {
-    const int i = tid + q * 64 * kW;
-    if (i < n_sdw) {
-      const int wr = i / (KB / 4), c = i % (KB / 4);
-      *reinterpret_cast<uint32_t*>(s_lds + (size_t)wr * KB + c * 4) = sreg[q];
+  for (int q = 0; q < SPAS; q++) {
+    const int j = tid + q * 64 * kW;
+    if (j < n_sq) {
+      if constexpr (SC16)
+        *reinterpret_cast<uint4*>(s_lds + (size_t)j * 16) = make_uint4(sreg[q][0], sreg[q][1], sreg[q][2], sreg[q][3]);
+      else
+        *reinterpret_cast<uint32_t*>(s_lds + (size_t)j * 4) = sreg[q][0];
     }
   }
   __builtin_amdgcn_s_waitcnt(gemv_wait_vm(INFL) & ~(15 << 8));  // + lgkmcnt(0)
@@ -335,10 +348,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
 // One launch per MLP half: whole lines for the dual gate/up pass, half lines
 // for down (measured at C1, T = 1 / T = 8, down: 4.42 / 5.22 us with whole
 // lines against 4.32 / 5.08 us; gate/up gains 0.15-0.2 us from them).
-template <bool DUAL, int NSTEP, int WPG>
+// SC16: the scale planes are 16-byte aligned (16-byte staging pieces).
+template <bool DUAL, int NSTEP, int WPG, bool SC16>
 __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  gemv_body<DUAL, NSTEP, WPG, DUAL>(g, blockIdx.x * (kW / WPG), lds);
+  gemv_body<DUAL, NSTEP, WPG, DUAL, SC16>(g, blockIdx.x * (kW / WPG), lds);
 }
 
 // Grouped (MoE) form: blockIdx.y is the group (expert).  Group e owns token
@@ -363,31 +377,37 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4_grouped(GemvArgs g, Grou
     g.b1 += e * gt.b_stride;
     g.s1 += e * gt.s_stride;
   }
-  gemv_body<DUAL, NSTEP, WPG, true>(g, blockIdx.x * (kW / WPG), lds);
+  gemv_body<DUAL, NSTEP, WPG, true, false>(g, blockIdx.x * (kW / WPG), lds);
 }
 
-template <bool DUAL, int NSTEP, int WPG>
+template <bool DUAL, int NSTEP, int WPG, bool SC16>
 static hipError_t launch_ns(const GemvArgs& g, hipStream_t st) {
   constexpr int NG = kW / WPG;
   static bool attr_set = false;  // allow up to 160 KB of dynamic LDS (once per instance)
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4<DUAL, NSTEP, WPG>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4<DUAL, NSTEP, WPG, SC16>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const int row_groups = DUAL ? g.n / 8 : g.n / 16;
-  hipLaunchKernelGGL((k_gemv_mxfp4<DUAL, NSTEP, WPG>), dim3(row_groups / NG), dim3(64 * kW),
+  hipLaunchKernelGGL((k_gemv_mxfp4<DUAL, NSTEP, WPG, SC16>), dim3(row_groups / NG), dim3(64 * kW),
                      gemv_lds_bytes(g.t, g.k, NG), st, g);
   return hipGetLastError();
 }
 
-template <bool DUAL, int WPG>
+template <bool DUAL, int WPG, bool SC16>
 static hipError_t launch_w(const GemvArgs& g, hipStream_t st) {
   const int per_wave = (g.k / kStepK + WPG - 1) / WPG;
-  if (per_wave <= 2) return launch_ns<DUAL, 2, WPG>(g, st);
-  if (per_wave <= 4) return launch_ns<DUAL, 4, WPG>(g, st);
-  return launch_ns<DUAL, 8, WPG>(g, st);
+  if (per_wave <= 2) return launch_ns<DUAL, 2, WPG, SC16>(g, st);
+  if (per_wave <= 4) return launch_ns<DUAL, 4, WPG, SC16>(g, st);
+  return launch_ns<DUAL, 8, WPG, SC16>(g, st);
+}
+
+template <bool SC16>
+static hipError_t launch_single(int dual, bool pair, const GemvArgs& g, hipStream_t st) {
+  if (dual) return launch_w<true, kW, SC16>(g, st);
+  return pair ? launch_w<false, kW / 2, SC16>(g, st) : launch_w<false, kW, SC16>(g, st);
 }
 
 // Preconditions (caller): 1 <= t <= 16, n % 16 == 0, k % 128 == 0 and
@@ -398,12 +418,15 @@ static hipError_t launch_w(const GemvArgs& g, hipStream_t st) {
 // x is then staged once for 32 rows (measured at C1 with HBM-cold weights:
 // 5.20 -> 5.11 us at T = 8, but 4.3 -> 4.5 us at T = 1).  The dual gate/up
 // GEMV keeps one group (its 256 workgroups would halve to 128, idling CUs).
+// Scale planes that are 16-byte aligned (the library's own allocations are)
+// are staged in 16-byte pieces; the C ABI also accepts 4-byte aligned ones,
+// which are staged in dwords.
 hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
   if (gemv_lds_bytes(g.t, g.k) > 160 * 1024 || g.k > 16384 || g.k % kStepK) return hipErrorInvalidValue;
   const bool pair = !dual && g.t >= 4 && (g.n / 16) % 2 == 0 && g.k <= 8192 &&
                     gemv_lds_bytes(g.t, g.k, 2) <= 160 * 1024;
-  if (dual) return launch_w<true, kW>(g, st);
-  return pair ? launch_w<false, kW / 2>(g, st) : launch_w<false, kW>(g, st);
+  const uintptr_t sp = reinterpret_cast<uintptr_t>(g.s0) | (dual ? reinterpret_cast<uintptr_t>(g.s1) : 0);
+  return sp % 16 == 0 ? launch_single<true>(dual, pair, g, st) : launch_single<false>(dual, pair, g, st);
 }
 
 size_t gemv_lds_need(int t, int k) { return gemv_lds_bytes(t, k); }

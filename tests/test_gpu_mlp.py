@@ -6,6 +6,7 @@ accumulates in float64).  Single matmuls are held to 1e-3 * rms.
 """
 import json
 import os
+import types
 
 import numpy as np
 import pytest
@@ -287,6 +288,33 @@ def test_decode_e8m0_255(dev, T, which):
         assert fin.sum() == T * (H - 2)
         rel, cos = O.mlp_error(got[fin], ref[fin])
         assert rel <= TOL and cos >= COS, (rel, cos)
+    d.free()
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_decode_scale_planes_4_byte_aligned(dev, T):
+    """The C ABI accepts scale planes that are only 4-byte aligned.  The
+    decode GEMV stages 16-byte aligned planes in 16-byte pieces and others
+    in dwords: copies of the same planes at a 4-byte offset must give the
+    same output bits."""
+    H, I = 1024, 2048
+    d = MlpData(dev, T, H, I, seed=71 + T)
+    ref = run_mlp(dev, d, M.MLP_FUSED)
+    shifted, mats = [], []
+    for q, s, n, k in d.mats:
+        host = dev.download(s, np.uint8, (n * (k // 32),))
+        buf = dev.upload(np.concatenate([np.zeros(4, np.uint8), host, np.zeros(12, np.uint8)]))
+        shifted.append(buf)
+        mats.append((q, types.SimpleNamespace(ptr=buf.ptr + 4)))
+    w = M.Device.weights(*mats)
+    out = dev.alloc(T * H * 2)
+    dev.mlp_forward(M.MLP_FUSED, T, H, I, d.x, w, out)
+    got = dev.download(out, np.float16, (T, H))
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    check(got, oracle_mlp(d, M.MLP_FUSED), what=f"decode T={T}, 4-byte aligned scale planes")
+    out.free()
+    for b in shifted:
+        b.free()
     d.free()
 
 
