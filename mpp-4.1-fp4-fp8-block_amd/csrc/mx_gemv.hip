@@ -136,15 +136,17 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
               reinterpret_cast<uint8_t*>(x_lds) + (size_t)t * (K + 8) * 2 + c * 1024);
     }
   }
-  // The rows' E8M0 bytes.  Passes wholly past them are skipped; inside the
-  // last pass, lanes past the end re-read the last piece (no predicated
-  // loads).  SC16 (the single launches): 16-byte pieces, each 8-row block
-  // (8 gate or 8 up channels, or 8 consecutive rows) being contiguous in
-  // memory and in LDS.  Otherwise (the grouped launches) dwords.  Measured:
-  // C1 T=1 gate/up 6.0 -> 5.68 us with pieces; the grouped launches at 64
-  // experts x 4 tokens went 199 -> 221 us (gate/up) and 97 -> 102 us
-  // (down) with pieces, so they keep dwords.  Skipping the passes past the
-  // scales took the C1 down pass from 4.27 to 3.94-3.99 us.
+  // The rows' E8M0 bytes.  Passes wholly past them are skipped (with SC16
+  // also waves wholly past them); inside the last pass or wave, lanes past
+  // the end re-read the last piece (no predicated loads).  SC16 (the single
+  // launches): 16-byte pieces, each 8-row block (8 gate or 8 up channels,
+  // or 8 consecutive rows) being contiguous in memory and in LDS.
+  // Otherwise (the grouped launches) dwords.  Measured at C1: gate/up 5.95
+  // -> 5.62 us with pieces, -> 5.28 us skipping idle waves (whose staging
+  // the barrier would wait for); the grouped launches at 64 experts x 4
+  // tokens went 199 -> 221 us (gate/up) and 97 -> 102 us (down) with
+  // pieces, so they keep dwords.  Skipping the passes past the scales took
+  // the C1 down pass from 4.27 to 3.94-3.99 us.
   constexpr int SPAS = SC16 ? scale_regs(NG) / 4 : scale_regs(NG);  // passes of 64 kW pieces
   const int QB = SC16 ? KB / 2 : 2 * KB;                             // pieces per 8-row block
   const int n_sq = 2 * NG * QB;                                      // pieces of the workgroup's rows
@@ -152,7 +154,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   uint32_t sreg[SPAS][PW];
 #pragma unroll
   for (int q = 0; q < SPAS; q++) {
-    if (q * 64 * kW >= n_sq) break;
+    if (q * 64 * kW + (SC16 ? wave * 64 : 0) >= n_sq) break;
     const int j = min(tid + q * 64 * kW, n_sq - 1);
     const int b = j / QB, o = j % QB;
     const uint8_t* w;
