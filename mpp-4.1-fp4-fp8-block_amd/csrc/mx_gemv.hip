@@ -136,22 +136,23 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
               reinterpret_cast<uint8_t*>(x_lds) + (size_t)t * (K + 8) * 2 + c * 1024);
     }
   }
-  // The rows' E8M0 bytes.  Passes wholly past them are skipped (with SC16
-  // also waves wholly past them); inside the last pass or wave, lanes past
-  // the end re-read the last piece (no predicated loads).  SC16 (the single
-  // launches): 16-byte pieces, each 8-row block (8 gate or 8 up channels,
-  // or 8 consecutive rows) being contiguous in memory and in LDS.
-  // Otherwise (the grouped launches) dwords.  Measured at C1: gate/up 5.95
-  // -> 5.62 us with pieces, -> 5.28 us skipping idle waves (whose staging
-  // the barrier would wait for); the grouped launches at 64 experts x 4
-  // tokens went 199 -> 221 us (gate/up) and 97 -> 102 us (down) with
-  // pieces, so they keep dwords.  Skipping the passes past the scales took
-  // the C1 down pass from 4.27 to 3.94-3.99 us.
+  // The rows' E8M0 bytes, one piece per thread and pass.  Each 8-row block
+  // (8 gate or 8 up channels, or 8 consecutive rows) is contiguous in
+  // memory and in LDS.  SC16 (the single launches): 16-byte pieces DMA'd
+  // straight to LDS; waves wholly past the pieces issue nothing and lanes
+  // past the end are masked.  Otherwise (the grouped launches): dwords
+  // through registers; passes wholly past the pieces are skipped and lanes
+  // past the end re-read the last dword (no predicated loads).  Measured at
+  // C1: gate/up 5.95 -> 5.62 us with 16-byte pieces, -> 5.28 us with the
+  // idle waves skipped (the staging barrier waits for every wave's loads),
+  // down 4.05 -> 4.0 us by DMA instead of through registers.  The grouped
+  // launches at 64 experts x 4 tokens went 199 -> 221 us (gate/up) and 97
+  // -> 102 us (down) with 16-byte pieces, so they keep dwords.  Skipping the
+  // dword passes past the scales took the C1 down pass from 4.27 to 3.94 us.
   constexpr int SPAS = SC16 ? scale_regs(NG) / 4 : scale_regs(NG);  // passes of 64 kW pieces
   const int QB = SC16 ? KB / 2 : 2 * KB;                             // pieces per 8-row block
   const int n_sq = 2 * NG * QB;                                      // pieces of the workgroup's rows
-  constexpr int PW = SC16 ? 4 : 1;                                   // dwords per piece
-  uint32_t sreg[SPAS][PW];
+  uint32_t sreg[SPAS][1];  // dword pieces (the 16-byte pieces go to LDS by DMA)
 #pragma unroll
   for (int q = 0; q < SPAS; q++) {
     if (q * 64 * kW + (SC16 ? wave * 64 : 0) >= n_sq) break;
@@ -160,9 +161,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
     const uint8_t* w;
     const uint8_t* s;
     row_ptrs(8 * b, w, s);
-    if constexpr (SC16) {
-      const uint4 v = *reinterpret_cast<const uint4*>(s + o * 16);
-      sreg[q][0] = v.x; sreg[q][1] = v.y; sreg[q][2] = v.z; sreg[q][3] = v.w;
+    if constexpr (SC16) {  // straight to LDS by DMA: lane l writes piece q 64 kW + 64 wave + l
+      if (tid + q * 64 * kW < n_sq) dma16(s + o * 16, s_lds + (size_t)(q * 64 * kW + wave * 64) * 16);
     } else {
       sreg[q][0] = *reinterpret_cast<const uint32_t*>(s + o * 4);
     }
@@ -214,17 +214,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   constexpr int INFL = ROLL ? 2 * RD : NSTEP;  // weight loads in flight at the staging wait
 
   // 3) Staging landed (only the INFL weight loads may still be in flight):
-  //    scales to LDS, then a bare barrier (__syncthreads would also wait for
-  //    the weights).
+  //    dword scales to LDS, then a bare barrier (__syncthreads would also
+  //    wait for the weights).
   __builtin_amdgcn_s_waitcnt(gemv_wait_vm(INFL));
 #pragma unroll
   for (int q = 0; q < SPAS; q++) {
     const int j = tid + q * 64 * kW;
     if (j < n_sq) {
-      if constexpr (SC16)
-        *reinterpret_cast<uint4*>(s_lds + (size_t)j * 16) = make_uint4(sreg[q][0], sreg[q][1], sreg[q][2], sreg[q][3]);
-      else
-        *reinterpret_cast<uint32_t*>(s_lds + (size_t)j * 4) = sreg[q][0];
+      if constexpr (!SC16) *reinterpret_cast<uint32_t*>(s_lds + (size_t)j * 4) = sreg[q][0];
     }
   }
   __builtin_amdgcn_s_waitcnt(gemv_wait_vm(INFL) & ~(15 << 8));  // + lgkmcnt(0)
