@@ -19,13 +19,14 @@
 //               same K permutation.  In the whole-line layout the loads move
 //               two steps of 8 rows (one 128-byte line each) and the lanes
 //               swap halves with a DPP rotate to get the same operands.
-//   order     = the activations (LDS DMA) and the rows' E8M0 scales are
-//               requested first, then the wave's weight loads (scheduling
-//               barriers keep the order): all of them, or, for whole lines
-//               with more than two line columns per wave, two columns with
-//               one more issued as each lands.  vmcnt retires in order, so
-//               the staging can be waited for and written to LDS while the
-//               weights are still in flight.
+//   order     = the activations (LDS DMA) and the rows' E8M0 scales (LDS
+//               DMA of 16-byte pieces in the single launches, dwords through
+//               registers in the grouped ones) are requested first, then the
+//               wave's weight loads (scheduling barriers keep the order): all
+//               of them, or, for whole lines with more than two line columns
+//               per wave, two columns with one more issued as each lands.
+//               vmcnt retires in order, so the staging can be waited for
+//               while the weights are still in flight.
 //   reduction = the W partial 16x16 tiles are added in LDS in wave order
 //               (deterministic, one barrier), then the epilogue writes f16:
 //                 single: out[t][n] = sum
@@ -43,8 +44,9 @@ namespace mx {
 constexpr int kStepK = 128;   // K per lane step: 4 lane groups x 32-element blocks
 // NSTEP: steps per wave whose weight loads are issued together (2, 4 or 8).
 constexpr int kW = 8;         // waves per workgroup
-// scale dwords staged per thread: 4 up to two row groups per workgroup
-// (K <= 16384), 8 for four and 16 for eight (launchers check K)
+// scale dwords staged per thread (a quarter as many 16-byte pieces): 4 up
+// to two row groups per workgroup (K <= 16384), 8 for four and 16 for eight
+// (launchers check K)
 constexpr int scale_regs(int ng) { return ng <= 2 ? 4 : ng <= 4 ? 8 : 16; }
 
 // 16-byte global -> LDS DMA of one lane (LDS base wave-uniform).
