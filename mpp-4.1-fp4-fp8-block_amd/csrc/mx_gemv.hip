@@ -140,17 +140,17 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   }
   // The rows' E8M0 bytes, one piece per thread and pass.  Each 8-row block
   // (8 gate or 8 up channels, or 8 consecutive rows) is contiguous in
-  // memory and in LDS.  SC16 (the single launches): 16-byte pieces DMA'd
+  // memory and in LDS.  SC16 (16-byte aligned planes): 16-byte pieces DMA'd
   // straight to LDS; waves wholly past the pieces issue nothing and lanes
-  // past the end are masked.  Otherwise (the grouped launches): dwords
-  // through registers; passes wholly past the pieces are skipped and lanes
-  // past the end re-read the last dword (no predicated loads).  Measured at
-  // C1: gate/up 5.95 -> 5.62 us with 16-byte pieces, -> 5.28 us with the
-  // idle waves skipped (the staging barrier waits for every wave's loads),
-  // down 4.05 -> 4.0 us by DMA instead of through registers.  The grouped
-  // launches at 64 experts x 4 tokens went 199 -> 221 us (gate/up) and 97
-  // -> 102 us (down) with 16-byte pieces, so they keep dwords.  Skipping the
-  // dword passes past the scales took the C1 down pass from 4.27 to 3.94 us.
+  // past the end are masked.  Otherwise: dwords through registers; passes
+  // wholly past the pieces are skipped and lanes past the end re-read the
+  // last dword (no predicated loads).  Measured at C1: gate/up 5.95 -> 5.62
+  // us with 16-byte pieces, -> 5.28 us with the idle waves skipped (the
+  // staging barrier waits for every wave's loads; whole waves re-reading one
+  // line had also made the grouped launches slower with pieces), down 4.05
+  // -> 4.0 us by DMA instead of through registers; 64 experts x 4 tokens
+  // 277.7 -> 269.8 us per MoE MLP.  Skipping the dword passes past the
+  // scales took the C1 down pass from 4.27 to 3.94 us.
   constexpr int SPAS = SC16 ? scale_regs(NG) / 4 : scale_regs(NG);  // passes of 64 kW pieces
   const int QB = SC16 ? KB / 2 : 2 * KB;                             // pieces per 8-row block
   const int n_sq = 2 * NG * QB;                                      // pieces of the workgroup's rows
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4(GemvArgs g) {
 // are bandwidth-bound, where fewer, whole-line requests pay (measured at 64
 // experts x 4 tokens of the C1 shape: 360 -> 297 us per MoE MLP, down alone
 // 113 -> 105 us).
-template <bool DUAL, int NSTEP, int WPG>
+template <bool DUAL, int NSTEP, int WPG, bool SC16>
 __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4_grouped(GemvArgs g, GroupTable gt) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int e = blockIdx.y;
@@ -378,7 +378,7 @@ __global__ __launch_bounds__(64 * kW) void k_gemv_mxfp4_grouped(GemvArgs g, Grou
     g.b1 += e * gt.b_stride;
     g.s1 += e * gt.s_stride;
   }
-  gemv_body<DUAL, NSTEP, WPG, true, false>(g, blockIdx.x * (kW / WPG), lds);
+  gemv_body<DUAL, NSTEP, WPG, true, SC16>(g, blockIdx.x * (kW / WPG), lds);
 }
 
 template <bool DUAL, int NSTEP, int WPG, bool SC16>
@@ -432,28 +432,43 @@ hipError_t launch_gemv_mxfp4(int dual, const GemvArgs& g, hipStream_t st) {
 
 size_t gemv_lds_need(int t, int k) { return gemv_lds_bytes(t, k); }
 
-template <bool DUAL, int NSTEP, int WPG>
+template <bool DUAL, int NSTEP, int WPG, bool SC16>
 static hipError_t launch_grouped_ns(const GemvArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
   constexpr int NG = kW / WPG;
   static bool attr_set = false;  // allow up to 160 KB of dynamic LDS (once per instance)
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4_grouped<DUAL, NSTEP, WPG>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_mxfp4_grouped<DUAL, NSTEP, WPG, SC16>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const int row_groups = DUAL ? g.n / 8 : g.n / 16;
-  hipLaunchKernelGGL((k_gemv_mxfp4_grouped<DUAL, NSTEP, WPG>), dim3(row_groups / NG, groups), dim3(64 * kW),
+  hipLaunchKernelGGL((k_gemv_mxfp4_grouped<DUAL, NSTEP, WPG, SC16>), dim3(row_groups / NG, groups), dim3(64 * kW),
                      gemv_lds_bytes(g.t, g.k, NG), st, g, gt);
   return hipGetLastError();
 }
 
-template <bool DUAL, int WPG>
+template <bool DUAL, int WPG, bool SC16>
 static hipError_t launch_grouped_w(const GemvArgs& g, const GroupTable& gt, int groups, hipStream_t st) {
   const int per_wave = (g.k / kStepK + WPG - 1) / WPG;
-  if (per_wave <= 2) return launch_grouped_ns<DUAL, 2, WPG>(g, gt, groups, st);
-  if (per_wave <= 4) return launch_grouped_ns<DUAL, 4, WPG>(g, gt, groups, st);
-  return launch_grouped_ns<DUAL, 8, WPG>(g, gt, groups, st);
+  if (per_wave <= 2) return launch_grouped_ns<DUAL, 2, WPG, SC16>(g, gt, groups, st);
+  if (per_wave <= 4) return launch_grouped_ns<DUAL, 4, WPG, SC16>(g, gt, groups, st);
+  return launch_grouped_ns<DUAL, 8, WPG, SC16>(g, gt, groups, st);
+}
+
+template <bool SC16>
+static hipError_t launch_grouped(int dual, int ng, const GemvArgs& g, const GroupTable& gt, int groups,
+                                 hipStream_t st) {
+  switch (ng) {
+    case 8: return dual ? launch_grouped_w<true, kW / 8, SC16>(g, gt, groups, st)
+                        : launch_grouped_w<false, kW / 8, SC16>(g, gt, groups, st);
+    case 4: return dual ? launch_grouped_w<true, kW / 4, SC16>(g, gt, groups, st)
+                        : launch_grouped_w<false, kW / 4, SC16>(g, gt, groups, st);
+    case 2: return dual ? launch_grouped_w<true, kW / 2, SC16>(g, gt, groups, st)
+                        : launch_grouped_w<false, kW / 2, SC16>(g, gt, groups, st);
+    default: return dual ? launch_grouped_w<true, kW, SC16>(g, gt, groups, st)
+                         : launch_grouped_w<false, kW, SC16>(g, gt, groups, st);
+  }
 }
 
 // g.t = the largest group's token count (sizes the LDS); the same
@@ -475,10 +490,13 @@ hipError_t launch_gemv_mxfp4_grouped(int dual, const GemvArgs& g, const GroupTab
   if (groups < 1 || groups > kMaxGroups || g.t < 1 || g.t > 16 || gemv_lds_bytes(g.t, g.k) > 160 * 1024 ||
       g.k > 16384 || g.k % kStepK)
     return hipErrorInvalidValue;
-  if (octo) return dual ? launch_grouped_w<true, kW / 8>(g, gt, groups, st) : launch_grouped_w<false, kW / 8>(g, gt, groups, st);
-  if (quad) return dual ? launch_grouped_w<true, kW / 4>(g, gt, groups, st) : launch_grouped_w<false, kW / 4>(g, gt, groups, st);
-  if (pair) return dual ? launch_grouped_w<true, kW / 2>(g, gt, groups, st) : launch_grouped_w<false, kW / 2>(g, gt, groups, st);
-  return dual ? launch_grouped_w<true, kW>(g, gt, groups, st) : launch_grouped_w<false, kW>(g, gt, groups, st);
+  const int ng = octo ? 8 : quad ? 4 : pair ? 2 : 1;
+  // 16-byte scale pieces when every group's planes are 16-byte aligned
+  // (64 experts x 4 tokens of the C1 shape: 277.7 -> 269.8 us per MoE MLP)
+  const uintptr_t sp = reinterpret_cast<uintptr_t>(g.s0) | (dual ? reinterpret_cast<uintptr_t>(g.s1) : 0) |
+                       gt.s_stride;
+  return sp % 16 == 0 ? launch_grouped<true>(dual, ng, g, gt, groups, st)
+                      : launch_grouped<false>(dual, ng, g, gt, groups, st);
 }
 
 }  // namespace mx

@@ -3,6 +3,8 @@ rows of one token batch, in two grouped launches.  Each expert is checked
 against the CPU oracle's MLP on that expert's rows and weights (BASELINE
 tolerance), on both the decode-GEMV form (<= 16 tokens per expert) and the
 small-M GEMM form, with empty experts in the mix."""
+import types
+
 import numpy as np
 import pytest
 
@@ -92,6 +94,28 @@ def test_moe_decode_experts(dev, counts, H, I):
         if cnt:
             check(got[t0:t0 + cnt], ref[t0:t0 + cnt], f"expert {e} ({cnt} tokens)")
         t0 += cnt
+    d.free()
+
+
+def test_moe_decode_scale_planes_4_byte_aligned(dev):
+    """The grouped decode GEMV stages 16-byte aligned scale planes in 16-byte
+    pieces and 4-byte aligned ones in dwords: copies of the same planes at a
+    4-byte offset give the same output bits."""
+    d = MoeData(dev, [3, 0, 5, 1, 16, 2], 512, 1024, seed=77)
+    ref = d.run()
+    shifted, mats = [], []
+    for q, s, n, k in d.mats:
+        host = dev.download(s, np.uint8, (n * (k // 32),))
+        buf = dev.upload(np.concatenate([np.zeros(4, np.uint8), host, np.zeros(12, np.uint8)]))
+        shifted.append(buf)
+        mats.append((q, types.SimpleNamespace(ptr=buf.ptr + 4)))
+    out = dev.alloc(d.T * d.H * 2)
+    dev.moe_forward(d.H, d.I, d.counts, d.x, M.Device.weights(*mats), out)
+    got = dev.download(out, np.float16, (d.T, d.H))
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    out.free()
+    for b in shifted:
+        b.free()
     d.free()
 
 
