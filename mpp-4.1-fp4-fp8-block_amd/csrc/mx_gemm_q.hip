@@ -330,23 +330,42 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 
   uint32_t scv[2][NWB];  // 4-bit scales of the stage in flight / in use
 
-  // SCL: the scale block [TBR rows][KT * KS/32 entries] into LDS, 2 bytes at a
-  // time (rows and entries are 2-byte aligned), before any DMA is issued.
+  // SCL: the scale block [TBR rows][KT * KS/32 entries] into LDS before any
+  // operand DMA is issued.  Rows of a whole number of dwords go by dword DMA
+  // (lane l of an instruction writes dword l of its 256 bytes); the deep
+  // ring then needs no wait of its own here, because its first stage wait
+  // and barrier also cover these older DMAs.  Other row lengths (and the
+  // 2-slot ring, which reads stage 0's scales before its first barrier)
+  // wait here.
   constexpr int ESZ = BK == BK_INT4G32 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? sc_lds_bytes(AK, NS) : 16];
   const int sc_row = KT * (KS / 32) * ESZ;  // bytes of one row's scales
   if constexpr (SCL) {
     static_assert(SCALES4, "scales in LDS are for 4-bit weights");
-    const int units = TBR * sc_row / 2;
-    for (int i = tid; i < units; i += 256) {
-      const int tr = i / (sc_row / 2), c = i % (sc_row / 2);
+    auto src_of = [&](int tr, int byte) {
       const int wrow = DUAL ? n0 + (tr & 63) : n0 + tr;
       const uint8_t* sb = reinterpret_cast<const uint8_t*>(DUAL && tr >= 64 ? g.s1 : g.s0);
-      const uint16_t v = *reinterpret_cast<const uint16_t*>(
-          sb + ((size_t)wrow * (K / 32) + (size_t)kt0 * (KS / 32)) * ESZ + (size_t)c * 2);
-      *reinterpret_cast<uint16_t*>(sc_lds + tr * sc_row + c * 2) = v;
+      return sb + ((size_t)wrow * (K / 32) + (size_t)kt0 * (KS / 32)) * ESZ + byte;
+    };
+    if (sc_row % 4 == 0 && (K / 32 * ESZ) % 4 == 0 && (kt0 * (KS / 32) * ESZ) % 4 == 0) {  // workgroup-uniform
+      const int dws = TBR * sc_row / 4;
+      for (int i0 = wave * 64; i0 < dws; i0 += 256) {  // wave-uniform
+        const int i = i0 + lane;
+        if (i < dws) dma4(src_of(i / (sc_row / 4), (i % (sc_row / 4)) * 4), sc_lds + (size_t)i0 * 4);
+      }
+      if constexpr (NS == 2) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    } else {
+      const int units = TBR * sc_row / 2;
+      for (int i = tid; i < units; i += 256) {
+        const int tr = i / (sc_row / 2), c = i % (sc_row / 2);
+        *reinterpret_cast<uint16_t*>(sc_lds + tr * sc_row + c * 2) =
+            *reinterpret_cast<const uint16_t*>(src_of(tr, c * 2));
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 
   // A of stage S into slot AS; the 4-bit scales of stage S into register set P.
