@@ -332,14 +332,15 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 
   // SCL: the scale block [TBR rows][KT * KS/32 entries] into LDS before any
   // operand DMA is issued.  Rows of a whole number of dwords go by dword DMA
-  // (lane l of an instruction writes dword l of its 256 bytes); the deep
-  // ring then needs no wait of its own here, because its first stage wait
-  // and barrier also cover these older DMAs.  Other row lengths (and the
-  // 2-slot ring, which reads stage 0's scales before its first barrier)
-  // wait here.
+  // (lane l of an instruction writes dword l of its 256 bytes) with no wait
+  // here: the deep ring's first stage wait and barrier also cover these
+  // older DMAs, and the 2-slot ring waits for them behind stage 0's operand
+  // DMAs, before it reads stage 0's scales.  Other row lengths wait here.
   constexpr int ESZ = BK == BK_INT4G32 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? sc_lds_bytes(AK, NS) : 16];
   const int sc_row = KT * (KS / 32) * ESZ;  // bytes of one row's scales
+  const bool sc_dma =                       // workgroup-uniform
+      SCL && sc_row % 4 == 0 && (K / 32 * ESZ) % 4 == 0 && (kt0 * (KS / 32) * ESZ) % 4 == 0;
   if constexpr (SCL) {
     static_assert(SCALES4, "scales in LDS are for 4-bit weights");
     auto src_of = [&](int tr, int byte) {
@@ -347,15 +348,11 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       const uint8_t* sb = reinterpret_cast<const uint8_t*>(DUAL && tr >= 64 ? g.s1 : g.s0);
       return sb + ((size_t)wrow * (K / 32) + (size_t)kt0 * (KS / 32)) * ESZ + byte;
     };
-    if (sc_row % 4 == 0 && (K / 32 * ESZ) % 4 == 0 && (kt0 * (KS / 32) * ESZ) % 4 == 0) {  // workgroup-uniform
+    if (sc_dma) {
       const int dws = TBR * sc_row / 4;
       for (int i0 = wave * 64; i0 < dws; i0 += 256) {  // wave-uniform
         const int i = i0 + lane;
         if (i < dws) dma4(src_of(i / (sc_row / 4), (i % (sc_row / 4)) * 4), sc_lds + (size_t)i0 * 4);
-      }
-      if constexpr (NS == 2) {
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
       }
     } else {
       const int units = TBR * sc_row / 2;
@@ -622,7 +619,16 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       MXQ_DEEP(0, f0, f1) MXQ_DEEP(1, f1, f0) MXQ_DEEP(2, f0, f1) MXQ_DEEP(3, f1, f0)
     }
   } else {
-  MXQ_ISSUE(0, a_s0, b_s0, 0)
+  MXQ_DMA_A(0, a_s0)
+  MXQ_DMA_B(0, b_s0)
+  if (sc_dma) {  // the scale DMAs (issued first) have landed; a bare barrier
+    __builtin_amdgcn_sched_barrier(0);
+    if (b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm(VM_A + NB));
+    else __builtin_amdgcn_s_waitcnt(wait_vm(VM_A));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  MXQ_SCALES(0, 0)
   if constexpr (BCH == 1) {
     int kt = 0;
     for (; kt + 2 <= KT; kt += 2) {
