@@ -1015,9 +1015,12 @@ int gemm_q_splits(int ak, int bk, int epi, int m, int n, int k) {
   // -> 16.0 us) and keeps two splits.
   if (bk == BK_MXFP4 && ak == AK_F16 && is_dual(epi) && kt <= 16 && tiles <= kDeepMaxWgs) return 1;
   int s = 1;
-  // (MXFP4 keeps the 2-slot split policy: C2's gate/up GEMM as 2 deep splits
-  // of 56 stages measured 2-3 us slower than 4 two-slot splits of 28)
-  if (deep_format(ak, bk) && bk != BK_MXFP4 && kt % 4 == 0) {
+  // MXFP4 gate/up GEMMs take the deep split policy too: C2's as 2 deep
+  // splits of 56 stages against 4 two-slot splits of 28 measured 72.4 ->
+  // 69.7 us (fused MLP, stream) and 67.4 -> 66.3 us (scaled) once the deep
+  // ring's scale staging went by DMA (2-3 us slower before).  MXFP4 store
+  // GEMMs keep the 2-slot policy.
+  if (deep_format(ak, bk) && (bk != BK_MXFP4 || is_dual(epi)) && kt % 4 == 0) {
     while (tiles * 2 * s <= kDeepMaxWgs && kt % (8 * s) == 0 && kt / (2 * s) >= 8) s *= 2;
     if (tiles * s >= 192) return s;  // else too few workgroups: the 2-slot policy below
     s = 1;
