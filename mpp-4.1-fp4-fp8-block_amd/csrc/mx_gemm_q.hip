@@ -196,6 +196,11 @@ constexpr int out_bytes(int epi) {
 // kScLds bytes) and read from there per stage.  Loaded per stage from global
 // memory instead, each stage waits for loads issued one stage earlier, whose
 // latency the short stages do not cover.
+// SCW (4-bit weights, f16 activations, chunked B, scales not in LDS): a
+// lane loads its row's scales for a whole B chunk (BCH stages) with one 8-
+// or 16-byte load issued beside the chunk's B DMA, instead of one element
+// per stage.  A per-stage element load touches 32 rows' lines per
+// instruction; the chunk load does that once per BCH stages.
 constexpr int kScLds = 16384;
 // F8X2 activations give 2 KB of it to the A slots' scale pairs, so that two
 // workgroups still share a CU (80 KB each).  Beside the deep ring (one
@@ -203,7 +208,7 @@ constexpr int kScLds = 16384;
 constexpr int sc_lds_bytes(int ak, int ns = 2) {
   return ns == 4 ? 49152 : ak == AK_F8X2 ? kScLds - 2048 : kScLds;
 }
-template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2, bool SCL = false>
+template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2, bool SCL = false, bool SCW = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
   constexpr bool DUAL = is_dual(EPI);
@@ -236,6 +241,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   static_assert(BCH == 1 || RBC == 128, "B chunks are whole 128-byte lines");
   static_assert(NS == 2 || (NS == 4 && BCH == 1 && (!SCALES4 || SCL) && !GROUPED),
                 "deep ring: per-stage B, 4-bit scales from LDS");
+  static_assert(!SCW || (SCALES4 && !SCL && NS == 2 && BCH > 1 && AK == AK_F16), "chunk scale loads");
   using AccT = typename std::conditional<AK == AK_I8, v16i, v16f>::type;
 
   // One __shared__ array per slot: the compiler then knows that a DMA into
@@ -365,6 +371,12 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     }
   }
 
+  // SCW: chunk scales by chunk parity, SCWD dwords per row (chunk C's
+  // element e of the lane's row is at byte e * ESZ of the chunk's bytes).
+  constexpr int SCWD = SCW ? BCH * (KS / 32) * ESZ / 4 : 1;
+  static_assert(!SCW || SCWD == 2 || SCWD == 4, "8- or 16-byte chunk scale loads");
+  uint32_t scw[2][NWB][SCWD];
+
   // A of stage S into slot AS; the 4-bit scales of stage S into register set P.
 #define MXQ_DMA_A(S, AS)                                                                           \
   {                                                                                                \
@@ -380,11 +392,34 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
         const uint8_t* p_ = sc_lds + (b_blk[j] + r32) * sc_row + ((S) * (KS / 32) + h) * ESZ;     \
         scv[P][j] = ESZ == 2 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_;  \
       }                                                                                            \
-    } else if (SCALES4) {                                                                          \
+    } else if (SCALES4 && !SCW) {                                                                  \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
         const uint8_t* p_ = sc_src[j] + (size_t)(S) * (KS / 32) * (BK == BK_INT4G32 ? 2 : 1);     \
         scv[P][j] = BK == BK_INT4G32 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_; \
       }                                                                                            \
+    }                                                                                              \
+  }
+  // SCW: chunk C's scales of the lane's rows into set Q; stage POS of the
+  // chunk in set Q into scv[P] (element POS * KS/32 + h).
+#define MXQ_SCW_LOAD(C, Q)                                                                         \
+  if constexpr (SCW) {                                                                             \
+    _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                               \
+      const uint8_t* p_ = sc_src[j] - h * ESZ + (size_t)(C) * (SCWD * 4);                          \
+      if constexpr (SCWD == 4) {                                                                   \
+        const uint4 v_ = *reinterpret_cast<const uint4*>(p_);                                      \
+        scw[Q][j][0] = v_.x; scw[Q][j][SCWD > 1 ? 1 : 0] = v_.y;                                   \
+        scw[Q][j][SCWD > 2 ? 2 : 0] = v_.z; scw[Q][j][SCWD > 3 ? 3 : 0] = v_.w;                    \
+      } else {                                                                                     \
+        const uint2 v_ = *reinterpret_cast<const uint2*>(p_);                                      \
+        scw[Q][j][0] = v_.x; scw[Q][j][SCWD > 1 ? 1 : 0] = v_.y;                                   \
+      }                                                                                            \
+    }                                                                                              \
+  }
+#define MXQ_SCW_PICK(Q, POS, P)                                                                    \
+  if constexpr (SCW) {                                                                             \
+    _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                               \
+      constexpr int e_ = (POS) * (KS / 32) * ESZ; /* byte of element POS * KS/32 (h = 0) */         \
+      scv[P][j] = (scw[Q][j][(e_ / 4) % SCWD] >> (8 * (e_ % 4) + 8 * ESZ * h)) & (ESZ == 2 ? 0xffffu : 0xffu); \
     }                                                                                              \
   }
   // B chunk C (stages C*BCH .. C*BCH + BCH - 1) into slot BS.
@@ -399,7 +434,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     }                                                                                              \
   }
   // loads one wave issues per stage (A + scales); a B chunk adds NB
-  constexpr int VM_A = NA + (SCALES4 && !SCL ? NWB : 0) + (AK == AK_F8X2 ? 1 : 0);
+  constexpr int VM_A = NA + (SCALES4 && !SCL && !SCW ? NWB : 0) + (AK == AK_F8X2 ? 1 : 0);
+  constexpr int VM_W = SCW ? NWB : 0;  // chunk scale loads, with a B chunk
 
   // One stage's MFMAs, in two halves.  MXQ_READ issues every LDS fragment
   // read of the stage into registers (AR, BR); MXQ_MATH widens the weights
@@ -557,12 +593,15 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       const int st_ = kt + (U);                                                                    \
       MXQ_DMA_A(min(st_ + 1, KT - 1), (AP_ ? a_s0 : a_s1))                                         \
       if (POS_ == 0) MXQ_DMA_B(min(st_ / BCH + 1, KT / BCH - 1), (BP_ ? b_s0 : b_s1))              \
+      if (POS_ == 0) MXQ_SCW_LOAD(min(st_ / BCH + 1, KT / BCH - 1), BP_ ^ 1)                       \
       MXQ_SCALES(min(st_ + 1, KT - 1), AP_ ^ 1)                                                    \
       __builtin_amdgcn_sched_barrier(0);                                                           \
-      if (POS_ == 0 && b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm(VM_A + NB));                   \
+      if (POS_ == 0 && b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm(VM_A + NB + VM_W));            \
+      else if (POS_ == 0) __builtin_amdgcn_s_waitcnt(wait_vm(VM_A + VM_W));                        \
       else __builtin_amdgcn_s_waitcnt(wait_vm(VM_A));                                              \
       __builtin_amdgcn_s_barrier();                                                                \
       __builtin_amdgcn_sched_barrier(0);                                                           \
+      MXQ_SCW_PICK(BP_, POS_, AP_)                                                                 \
       MXQ_COMPUTE((AP_ ? a_s1 : a_s0), (BP_ ? b_s1 : b_s0), AP_, POS_)                             \
       __builtin_amdgcn_s_barrier();                                                                \
     }                                                                                              \
@@ -621,6 +660,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   } else {
   MXQ_DMA_A(0, a_s0)
   MXQ_DMA_B(0, b_s0)
+  MXQ_SCW_LOAD(0, 0)
   if (sc_dma) {  // the scale DMAs (issued first) have landed; a bare barrier
     __builtin_amdgcn_sched_barrier(0);
     if (b_issuer) __builtin_amdgcn_s_waitcnt(wait_vm(VM_A + NB));
@@ -663,6 +703,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 #undef MXQ_DMA_A
 #undef MXQ_DMA_B
 #undef MXQ_SCALES
+#undef MXQ_SCW_LOAD
+#undef MXQ_SCW_PICK
 #undef MXQ_COMPUTE
 #undef MXQ_MATH_FORM
 #undef MXQ_MATH_F8X2
@@ -888,6 +930,19 @@ template <int AK, int BK, int NWB, int NS = 2> bool sc_lds_fits(int kt) {
   return NWB * 64 * kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1) <= sc_lds_bytes(AK, NS);
 }
 
+// True when the chunk scale loads (SCW) are aligned: every row's scales, the
+// planes and the per-group stride a multiple of a chunk's scale bytes (split
+// starts are whole chunks).
+template <int AK, int BK> bool scw_ok(const QGemmArgs& g, bool dual, size_t s_stride) {
+  if constexpr (AK != AK_F16 || !(BK == BK_MXFP4 || BK == BK_INT4G32)) {
+    return false;
+  } else {
+    constexpr size_t cb = b_chunk<AK, BK>() * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1);
+    const size_t row = (size_t)g.k / 32 * (BK == BK_INT4G32 ? 2 : 1);
+    return row % cb == 0 && s_stride % cb == 0 && (uintptr_t)g.s0 % cb == 0 && (!dual || (uintptr_t)g.s1 % cb == 0);
+  }
+}
+
 // Launches of at most this many workgroups (one per CU) take the deep ring,
 // for weight formats staged per stage whose four slots fit the 160 KB of LDS
 // (not f32 activations x f16 weights: 4 x 48 KB).  MXFP4 weights under f16
@@ -940,7 +995,10 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   constexpr bool S4 = BK == BK_MXFP4 || BK == BK_INT4G32;
   const bool scl = S4 && sc_lds_fits<AK, BK, NWB>(kt);
   if (BC > 1 && kt % BC == 0 && kt >= 4 * BC) {
+    constexpr bool W = AK == AK_F16 && S4 && BC > 1;
     if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC, 2, S4>), grid, dim3(256), 0, st, g, 0);
+    else if (W && scw_ok<AK, BK>(g, is_dual(EPI), 0))
+      hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC, 2, false, W>), grid, dim3(256), 0, st, g, 0);
     else hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, BC>), grid, dim3(256), 0, st, g, 0);
   } else {
     if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 2, S4>), grid, dim3(256), 0, st, g, 0);
@@ -983,6 +1041,8 @@ hipError_t launch_q_grouped(const QGemmArgs& g0, const GroupTable& gt, int group
   const bool scl = sc_lds_fits<AK, BK, NWB>(kt);  // MXFP4 only here
   if (BC > 1 && kt % BC == 0 && kt >= 4 * BC) {
     if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, BC, 2, true>), grid, dim3(256), 0, st, g, gt);
+    else if (scw_ok<AK, BK>(g, is_dual(EPI), gt.s_stride))
+      hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, BC, 2, false, true>), grid, dim3(256), 0, st, g, gt);
     else hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, BC>), grid, dim3(256), 0, st, g, gt);
   } else {
     if (scl) hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, true, 1, 2, true>), grid, dim3(256), 0, st, g, gt);

@@ -157,6 +157,37 @@ def test_moe_gemm_large_groups(dev):
     d.free()
 
 
+def test_moe_gemm_long_k_chunk_scales(dev):
+    """Grouped gate/up GEMM at H=7168: its E8M0 scales (28 KB per workgroup)
+    do not fit the LDS copy, so each lane loads a B chunk's scales with one
+    8-byte load.  Sampled tokens against the oracle; the same planes copied
+    to a 4-byte offset take the per-stage byte loads and give the same bits."""
+    counts, H, I = [40, 0, 150, 17], 7168, 256
+    d = MoeData(dev, counts, H, I, seed=93)
+    got = d.run()
+    rows, t0 = [], 0
+    for cnt in counts:
+        if cnt:
+            rows += [t0, t0 + cnt // 2, t0 + cnt - 1]
+        t0 += cnt
+    ref = d.oracle(rows=rows)
+    check(got[rows], ref[rows], f"H={H} sampled tokens")
+    shifted, mats = [], []
+    for q, s, n, k in d.mats:
+        host = dev.download(s, np.uint8, (n * (k // 32),))
+        buf = dev.upload(np.concatenate([np.zeros(4, np.uint8), host, np.zeros(12, np.uint8)]))
+        shifted.append(buf)
+        mats.append((q, types.SimpleNamespace(ptr=buf.ptr + 4)))
+    out = dev.alloc(d.T * d.H * 2)
+    dev.moe_forward(d.H, d.I, d.counts, d.x, M.Device.weights(*mats), out)
+    moved = dev.download(out, np.float16, (d.T, d.H))
+    assert np.array_equal(moved.view(np.uint16), got.view(np.uint16))
+    out.free()
+    for b in shifted:
+        b.free()
+    d.free()
+
+
 def test_moe_one_expert_is_the_decode_mlp(dev):
     """One expert through the grouped GEMV runs the same arithmetic as the
     ungrouped decode GEMV: bit-identical to mx_mlp_forward.  T = 3 keeps
