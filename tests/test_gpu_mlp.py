@@ -214,6 +214,17 @@ def test_config2_fused_and_dequant(dev):
     d.free()
 
 
+def test_fused_gate_up_chunk_scales(dev):
+    """Fused MLP whose gate/up GEMM has more workgroups than CUs (288 tiles,
+    2-slot ring) and 28 KB of E8M0 scales per workgroup (K = 8192): the
+    scales are loaded per 4-stage B chunk, one 8-byte load per lane."""
+    T, H, I = 2304, 8192, 1024
+    d = MlpData(dev, T, H, I, seed=29)
+    rows = sample_rows(T, 12)
+    check(run_mlp(dev, d, M.MLP_FUSED)[rows], oracle_mlp(d, M.MLP_FUSED, rows=rows), what="fused, chunk scales")
+    d.free()
+
+
 def test_w4a4_ragged_scale_tiles(dev):
     """W4A4 with more than 2^20 weight-scale dwords (the tiled stage-major
     conversion) and stage counts that leave partial 32-stage tiles (gate/up
