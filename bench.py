@@ -118,7 +118,7 @@ def make_sets(dev, M, T, H, I, n_sets, seed, wfmt=0):
     return x, sets, bufs
 
 
-def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt=0, cpu=None):
+def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt=0, cpu=None, cpu_flop_cap=1e11):
     """Time `iters` forwards twice: replayed from one HIP graph (the value;
     the reference likewise pre-encodes all iterations in one command buffer)
     and launched one by one on the stream (reported as stream_us_per_iter).
@@ -144,7 +144,7 @@ def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt
            "stream_us_per_iter": round(ssecs / iters * 1e6, 3),
            "kernel_us": {k: round(v, 3) for k, v in kern.items()}}
     if cpu:
-        res["cpu_baseline"] = cpu_row(dev, M, variant, wfmt, T, H, I, x, bufs[:6], out, cpu)
+        res["cpu_baseline"] = cpu_row(dev, M, variant, wfmt, T, H, I, x, bufs[:6], out, cpu, flop_cap=cpu_flop_cap)
     for b in bufs + [x, out]:
         b.free()
     log(f"[bench] {name}: {us:.2f} us/iter (stream {res['stream_us_per_iter']}), "
@@ -188,7 +188,7 @@ def run_moe(dev, M, name, E, per_expert, H, I, iters, warmup, seed):
 CPU_THREADS = 16  # the GPU box's CPU share for one GPU (its nproc may show more)
 
 
-def cpu_row(dev, M, variant, wfmt, T, H, I, x, wbufs, out, tokens, budget_s=12.0):
+def cpu_row(dev, M, variant, wfmt, T, H, I, x, wbufs, out, tokens, budget_s=12.0, flop_cap=1e11):
     """The CPU baseline of one configuration, on that GPU row's own inputs:
     x and weight set 0 are downloaded, and the CPU port (oracle/mx_oracle.c,
     the reference's one-output-per-dot-product loop restated,
@@ -196,7 +196,9 @@ def cpu_row(dev, M, variant, wfmt, T, H, I, x, wbufs, out, tokens, budget_s=12.0
     dequantize-then-FP32-accumulate semantics) runs the first `tokens`
     tokens on CPU_THREADS host threads.  A sample smaller than T is scaled
     to the whole job and labelled extrapolated.  Its output is checked
-    against the GPU's for the same tokens (max-abs / rms, cosine)."""
+    against the GPU's for the same tokens (max-abs / rms, cosine).  The
+    sample stops at `budget_s` seconds or `flop_cap` flops, whichever
+    comes first."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -235,7 +237,7 @@ def cpu_row(dev, M, variant, wfmt, T, H, I, x, wbufs, out, tokens, budget_s=12.0
             ref = run()
             n += 1
             el = time.perf_counter() - t0
-            if el >= budget_s or flops * (n + 1) > 1e11:
+            if el >= budget_s or flops * (n + 1) > flop_cap:
                 break
     finally:
         O.set_accum_f32(False)
@@ -316,7 +318,8 @@ def main():
     # ---- headline: config 1, T=1 ------------------------------------------
     T, H, I = 1, 7168, 2048
     prim, _ = run_config(dev, M, "C1 T=1 fused", M.MLP_FUSED, T, H, I, 24, args.steps,
-                         args.warmup, seed=1, cpu=None if args.no_cpu else T)
+                         args.warmup, seed=1, cpu=None if args.no_cpu else T,
+                         cpu_flop_cap=4e11)  # about 12 s of host work for the headline sample
     us = prim["us_per_iter"]
     # algorithmic bytes per launch of each kernel the decode MLP may run:
     # weights + E8M0 scales + activations in + results out (for the whole
