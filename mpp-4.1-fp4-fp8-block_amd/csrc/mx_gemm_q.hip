@@ -1015,7 +1015,9 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
 // 12.6 us per step with its reduce, 12.25 -> 11.5 us on the F8X2 path; C3
 // INT4's down GEMM, N = 4096: the MLP 96.8 -> 94.1 us in stream mode).
 // Other formats measured no gain (C3) or a loss (C2 dequant, f16 weights:
-// +2.5 us).
+// +2.5 us).  C2's MXFP4 down GEMM on 64-row tiles (448 two-slot workgroups
+// instead of 224 on the deep ring): fused 23.6 -> 24.9 us; scaled 20.2 ->
+// 18.7 us but the scaled MLP unchanged (66.1-67.1 against 67.0-67.3 us).
 inline bool wide_tiles(int bk, int epi, int n) {
   return !is_dual(epi) && n % 128 == 0 && !(bk == BK_MXFP4 && n / 128 < 16) &&
          !(bk == BK_INT4G32 && n / 128 < 64);
