@@ -5,6 +5,8 @@ i8_i8_i32 (MPPMLPKernels.metal:50-125), unscaled in the reference; BASELINE
 adds per-row (FP8, INT8) and per-32 f16 (INT4) scales.  Quantizers must be
 bit-exact with the oracle; MLP outputs within the BASELINE tolerance.
 """
+import types
+
 import numpy as np
 import pytest
 
@@ -97,4 +99,29 @@ def test_config3_formats(dev, wfmt):
     rel, cos = O.mlp_error(got, oracle_fmt(d, wfmt, rows=rows))
     print(f"C3 fmt {wfmt}: rel={rel:.3e} cos={cos:.7f}", flush=True)
     assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    d.free()
+
+
+def test_int4_scale_planes_4_byte_aligned(dev):
+    """INT4 gate/up GEMM with 224 tiles and 32 KB of f16 scales per
+    workgroup: 16-byte aligned planes load a B chunk's scales with one
+    16-byte load per lane, planes at a 4-byte offset one scale per stage.
+    Same output bits."""
+    T, H, I = 32, 4096, 14336
+    d = MlpData(dev, T, H, I, seed=41, wfmt=M.WFMT_INT4)
+    ref = run_fmt(dev, d, M.WFMT_INT4)
+    shifted, mats = [], []
+    for q, s, n, k in d.mats:
+        host = dev.download(s, np.uint8, (n * (k // 32) * 2,))
+        buf = dev.upload(np.concatenate([np.zeros(4, np.uint8), host, np.zeros(12, np.uint8)]))
+        shifted.append(buf)
+        mats.append((q, types.SimpleNamespace(ptr=buf.ptr + 4)))
+    out = dev.alloc(T * H * 2)
+    dev.fmt_mlp_forward(M.WFMT_INT4, T, H, I, d.x, M.Device.weights(*mats), out)
+    got = dev.download(out, np.float16, (T, H))
+    assert np.isfinite(ref.astype(np.float64)).all()
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    out.free()
+    for b in shifted:
+        b.free()
     d.free()
