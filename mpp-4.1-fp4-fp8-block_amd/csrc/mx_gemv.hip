@@ -344,7 +344,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
 #pragma unroll
     for (int w = 0; w < WPG; w++) tot += red[((g2 * WPG + w) * 16 + tt) * 17 + cc];
     if (DUAL) {
-      const float uv = __shfl_xor(tot, 8);  // column cc + 8 is the same channel's up sum
+      // column cc + 8 is the same channel's up sum: lanes cc and cc ^ 8 of
+      // each 16-lane row swap by DPP row_ror:8 (no LDS round trip)
+      const float uv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, tot), 0x128, 0xf, 0xf, false));
       if (cc < 8 && tt < T) g.out[(size_t)tt * g.n + grp * 8 + cc] = f32_to_f16_bits(silu(tot) * uv);
     } else if (tt < T) {
       g.out[(size_t)tt * g.n + grp * 16 + cc] = f32_to_f16_bits(tot);
