@@ -230,7 +230,12 @@ def test_format_mlp_vs_numpy():
         g, u = xf @ deq[0].T, xf @ deq[1].T
         ref = (g / (1 + np.exp(-g)) * u) @ deq[2].T
         rel, cos = O.mlp_error(out, ref)
-        tol = 5e-2 if fmt == O.WF_W8A8 else O.MAX_ABS_REL_TOL
+        # FP8 / INT8 / INT4: the same dequantized weights on both sides, so the
+        # gap is the oracle's float32 accumulation and f16 output rounding
+        # (measured 0.7e-3 to 1.3e-3 of rms over several seeds).  W8A8 also
+        # quantizes x and mid to int8, which this float64 MLP does not; its
+        # composition is pinned exactly in test_oracle_w8a8.py.
+        tol = 5e-2 if fmt == O.WF_W8A8 else 3e-3
         assert rel <= tol and cos >= 0.999, (fmt, rel, cos)
 
 
