@@ -220,10 +220,20 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, int g0, uint8_t* ld
   else
     load_batch(gw);
   constexpr int INFL = ROLL ? 2 * RD : NSTEP;  // weight loads in flight at the staging wait
+  static_assert(!TSKIP || WL, "skipped columns are whole-line columns");
 
   // 3) Staging landed (only the INFL weight loads may still be in flight):
   //    dword scales to LDS, then a bare barrier (__syncthreads would also
-  //    wait for the weights).
+  //    wait for the weights).  With TSKIP a wave near the end of K issues
+  //    fewer than INFL weight loads (none when its first column is past the
+  //    last one), so vmcnt(INFL) would not cover its staging loads: such a
+  //    wave waits for all of its loads.  The count is wave-uniform (a
+  //    scalar branch around the extra wait).
+  if constexpr (TSKIP) {
+    const int first = ROLL ? RD : NLC;  // columns the first batch may issue
+    const int cols = __builtin_amdgcn_readfirstlane(min(first, max(0, (LC - gw + WPG - 1) / WPG)));
+    if (2 * cols < INFL) __builtin_amdgcn_s_waitcnt(gemv_wait_vm(0));
+  }
   __builtin_amdgcn_s_waitcnt(gemv_wait_vm(INFL));
 #pragma unroll
   for (int q = 0; q < SPAS; q++) {
