@@ -157,11 +157,14 @@ int mx_mxfp4_dequant_f16(mx_ctx* ctx, const uint8_t* packed, const uint8_t* scal
 /* ---- matmuls -------------------------------------------------------------- */
 /* C[m][n] = sum_k A[m][k] * fp4(B[n][k]) * 2^(S[n][k/32]-127):
  * mxfp4_native_sp_h_f_n64 / mxfp4_fused_h_f_n64 (MXFP4Kernels.metal:108-130,
- * 264-286; ABI a, b, c, m, n, k, scales).  a f16; c f32 or f16. */
+ * 264-286; ABI a, b, c, m, n, k, scales).  a f16 or f32; c f32 or f16.
+ * Any m, n >= 1 (the reference's tiles guard column < n,
+ * MXFP4Kernels.metal:98); k % 32 == 0. */
 int mx_mxfp4_matmul(mx_ctx* ctx, const void* a, int a_dtype, const uint8_t* b, void* c,
                     int c_dtype, int m, int n, int k, const uint8_t* scales);
 /* C f32 = A * B^T with B f16 [n][k]: mpp_mlp_h_h_f_n128 (a f16) and
- * mpp_mlp_f_h_f_n128 (a f32) (MPPMLPKernels.metal:39-48, 164-173). */
+ * mpp_mlp_f_h_f_n128 (a f32) (MPPMLPKernels.metal:39-48, 164-173).
+ * Any m, n >= 1; k % 32 == 0. */
 int mx_gemm_f16(mx_ctx* ctx, const void* a, int a_dtype, const void* b, float* c, int m, int n,
                 int k);
 /* C i32 = A * B^T with A int8 [m][k], B int8 [n][k], exact i32 sums:
@@ -194,9 +197,10 @@ int mx_swiglu(mx_ctx* ctx, const void* gate, const void* up, void* mid, const mx
 /* ---- MLP ------------------------------------------------------------------ */
 /* down(silu(gate(x)) * up(x)).  x f16 [T][H]; weights MXFP4; out f16 [T][H]
  * (f32 for MX_MLP_REFROW).  Validation as runMLPBenchmark (main.swift:592-597):
- * positive sizes, hidden/intermediate % 32 (MXFP4 rows, :1043); W4A4 also
- * needs hidden and intermediate % 128.  The reference's tokens % 64 rule
- * (:946) is lifted.  Scratch memory is owned by the context. */
+ * positive sizes, hidden and intermediate % 32 (the MXFP4 rows, :1043) for
+ * FUSED, DEQUANT and REFROW; SCALED needs % 64 and W4A4 % 128.  The
+ * reference's tokens % 64 rule (:946) is lifted.  Scratch memory is owned by
+ * the context. */
 int mx_mlp_forward(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const void* x,
                    const mx_mlp_weights* w, void* out);
 
@@ -277,7 +281,8 @@ int mx_load_mxfp4(mx_ctx* ctx, const char* path, const char* blocks_name, const 
 int mx_fmt_quantize(mx_ctx* ctx, int wfmt, const float* w, int rows, int k, void* q,
                     void* scales);
 /* MLP with format weights: mpp_mlp_h_fp8e4m3_f_n128 / _h_fp8e5m2_f_n128 /
- * h_i8_f / h_i4_f / i8_i8_i32 rows (MPPMLPKernels.metal:50-125) with scales. */
+ * h_i8_f / h_i4_f / i8_i8_i32 rows (MPPMLPKernels.metal:50-125) with scales.
+ * hidden and intermediate % 32; W8A8 % 128. */
 int mx_fmt_mlp_forward(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,
                        const mx_mlp_weights* w, void* out);
 int mx_fmt_mlp_benchmark(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,

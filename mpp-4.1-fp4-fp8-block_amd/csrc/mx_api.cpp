@@ -91,6 +91,20 @@ int ensure_ws(mx_ctx* c, size_t bytes) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Split-K partial bytes of a GEMM that the 64-K-stage family takes (0 when
+// the shape goes to the K-step-32 kernel, which does not split K).
+size_t q_ws(int ak, int bk, int epi, int m, int n, int k) {
+  return mx::gemm_q_ok(ak, bk, epi, m, n, k) ? mx::gemm_q_ws_bytes(ak, bk, epi, m, n, k) : 0;
+}
+
+// One GEMM of an MLP: the 64-K-stage family when the shape fits it, else the
+// K-step-32 kernel (any n, k % 32 == 0).
+hipError_t launch_mlp_gemm(int ak, int bk, int epi, const mx::QGemmArgs& q, hipStream_t st) {
+  if (mx::gemm_q_ok(ak, bk, epi, q.m, q.n, q.k)) return mx::launch_gemm_q(ak, bk, epi, q, st);
+  mx::GemmArgs g{q.a, ak == mx::AK_F32 ? MX_DTYPE_F32 : MX_DTYPE_F16, q.b0, q.s0, q.b1, q.s1, q.c, q.m, q.n, q.k};
+  return mx::launch_gemm_h(bk, epi, g, st);
+}
+
 // A forward pass as a list of launches (so the benchmark can time each).
 struct Step {
   const char* name;
@@ -107,8 +121,11 @@ int check_mlp_cfg(mx_ctx* c, int variant, const mx_mlp_config* cfg) {
                    "MLP hidden and intermediate sizes must be multiples of 16 for packed FP4 weights.");
   if (H % 32 || I % 32)
     return set_err(c, MX_EINVAL, "MXFP4 rows need hidden and intermediate to be multiples of 32.");
-  if (H % 64 || I % 64)
-    return set_err(c, MX_EINVAL, "hidden and intermediate must be multiples of 64 (MFMA tile).");
+  // The reference's MXFP4 rows need only % 32 (main.swift:1043); so do
+  // FUSED, REFROW and DEQUANT.  The scaled-MFMA variant splits x and mid in
+  // 64-K groups.
+  if (variant == MX_MLP_SCALED && (H % 64 || I % 64))
+    return set_err(c, MX_EINVAL, "The scaled variant needs hidden and intermediate to be multiples of 64.");
   if (variant == MX_MLP_W4A4 && (H % 128 || I % 128))
     return set_err(c, MX_EINVAL, "W4A4 needs hidden and intermediate to be multiples of 128.");
   if (variant < MX_MLP_FUSED || variant > MX_MLP_SCALED)
@@ -126,12 +143,18 @@ bool gemv_ok(const mx_mlp_config* cfg) {
 }
 
 // Which kernels a forward runs (shared by the launcher and the name query).
-enum MlpPath { PATH_GEMV, PATH_GEMM_Q, PATH_REFROW, PATH_DEQUANT, PATH_W4A4, PATH_SCALED };
+// PATH_GEMM_H: the fused (or reference-row) MLP at shapes the 64-K-stage
+// family does not take (hidden or intermediate % 64 != 0): both GEMMs on the
+// K-step-32 kernel.
+enum MlpPath { PATH_GEMV, PATH_GEMM_Q, PATH_REFROW, PATH_DEQUANT, PATH_W4A4, PATH_SCALED, PATH_GEMM_H,
+               PATH_REFROW_H };
+
+bool q_shapes(const mx_mlp_config* cfg) { return cfg->hidden % 64 == 0 && cfg->intermediate % 64 == 0; }
 
 MlpPath mlp_path(int variant, const mx_mlp_config* cfg) {
   switch (variant) {
-    case MX_MLP_FUSED: return gemv_ok(cfg) ? PATH_GEMV : PATH_GEMM_Q;
-    case MX_MLP_REFROW: return PATH_REFROW;
+    case MX_MLP_FUSED: return gemv_ok(cfg) ? PATH_GEMV : q_shapes(cfg) ? PATH_GEMM_Q : PATH_GEMM_H;
+    case MX_MLP_REFROW: return q_shapes(cfg) ? PATH_REFROW : PATH_REFROW_H;
     case MX_MLP_DEQUANT: return PATH_DEQUANT;
     case MX_MLP_SCALED: return PATH_SCALED;
     default: return PATH_W4A4;
@@ -155,8 +178,8 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
   if (variant == MX_MLP_FUSED || variant == MX_MLP_REFROW) {
     s.mid = take(T * I * 2);
     const int e = variant == MX_MLP_REFROW ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16;
-    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_MXFP4, e, (int)T, (int)I, (int)H),
-                          mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_MXFP4, mx::EPI_STORE_F32, (int)T, (int)H, (int)I)));
+    s.qws = take(std::max(q_ws(mx::AK_F16, mx::BK_MXFP4, e, (int)T, (int)I, (int)H),
+                          q_ws(mx::AK_F16, mx::BK_MXFP4, mx::EPI_STORE_F32, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_SCALED) {
     s.xq = take(mx::f8x2_data_bytes(T, H));
     s.xe = take(mx::f8x2_e8_bytes(T, H));
@@ -171,8 +194,8 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
     s.gate = take(T * I * 4);
     s.up = take(T * I * 4);
     s.mid = take(T * I * 4);
-    s.qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, (int)T, (int)I, (int)H),
-                          mx::gemm_q_ws_bytes(mx::AK_F32, mx::BK_F16, mx::EPI_STORE_F16, (int)T, (int)H, (int)I)));
+    s.qws = take(std::max(q_ws(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, (int)T, (int)I, (int)H),
+                          q_ws(mx::AK_F32, mx::BK_F16, mx::EPI_STORE_F16, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_W4A4) {
     s.xq = take(T * H / 2);
     s.mq = take(T * I / 2);
@@ -239,6 +262,18 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
     mx::GemvArgs dn{mid, wd, sd, nullptr, nullptr, static_cast<uint16_t*>(out), T, H, I};
     steps.push_back({"gemv_mxfp4_gate_up_swiglu", [=] { return mx::launch_gemv_mxfp4(1, gu, st); }});
     steps.push_back({"gemv_mxfp4_down", [=] { return mx::launch_gemv_mxfp4(0, dn, st); }});
+  } else if (path == PATH_GEMM_H || path == PATH_REFROW_H) {
+    // hidden or intermediate % 64 != 0: both GEMMs on the K-step-32 kernel
+    uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
+    const bool ref = path == PATH_REFROW_H;
+    const int e_gu = ref ? mx::EPI_SWIGLU_HALF : mx::EPI_SWIGLU_F16;
+    const int e_dn = ref ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
+    mx::GemmArgs gu{x, MX_DTYPE_F16, wg, sg, wu, su, mid, T, I, H};
+    mx::GemmArgs dn{mid, MX_DTYPE_F16, wd, sd, nullptr, nullptr, out, T, H, I};
+    steps.push_back({ref ? "gemm_h_mxfp4_gate_up_swiglu_half" : "gemm_h_mxfp4_gate_up_swiglu",
+                     [=] { return mx::launch_gemm_h(mx::BK_MXFP4, e_gu, gu, st); }});
+    steps.push_back({ref ? "gemm_h_mxfp4_down_f32" : "gemm_h_mxfp4_down",
+                     [=] { return mx::launch_gemm_h(mx::BK_MXFP4, e_dn, dn, st); }});
   } else if (path == PATH_GEMM_Q || path == PATH_REFROW) {
     uint16_t* mid = reinterpret_cast<uint16_t*>(ws + s.mid);
     const bool ref = path == PATH_REFROW;
@@ -283,10 +318,10 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
     mx::QGemmArgs gg{x, nullptr, wg16, nullptr, nullptr, nullptr, gate, qws, T, I, H, 0};
     mx::QGemmArgs gp{x, nullptr, wu16, nullptr, nullptr, nullptr, up, qws, T, I, H, 0};
     mx::QGemmArgs dn{mid, nullptr, wd16, nullptr, nullptr, nullptr, out, qws, T, H, I, 0};
-    steps.push_back({"gemm_h_h_f_gate", [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, gg, st); }});
-    steps.push_back({"gemm_h_h_f_up", [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, gp, st); }});
+    steps.push_back({"gemm_h_h_f_gate", [=] { return launch_mlp_gemm(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, gg, st); }});
+    steps.push_back({"gemm_h_h_f_up", [=] { return launch_mlp_gemm(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, gp, st); }});
     steps.push_back({"swiglu_float", [=] { return mx::launch_swiglu(0, gate, up, mid, (size_t)T * I, st); }});
-    steps.push_back({"gemm_f_h_down", [=] { return mx::launch_gemm_q(mx::AK_F32, mx::BK_F16, mx::EPI_STORE_F16, dn, st); }});
+    steps.push_back({"gemm_f_h_down", [=] { return launch_mlp_gemm(mx::AK_F32, mx::BK_F16, mx::EPI_STORE_F16, dn, st); }});
   } else {  // W4A4
     uint8_t* xq = ws + s.xq;
     uint8_t* xs = ws + s.xs;
@@ -558,9 +593,10 @@ int mx_mxfp4_dequant_f16(mx_ctx* c, const uint8_t* packed, const uint8_t* scales
   return MX_OK;
 }
 
+// Any n (the reference's tiles guard column < n, MXFP4Kernels.metal:98);
+// k % 32 (one E8M0 block).
 static int check_gemm(mx_ctx* c, int m, int n, int k, const void* a, const void* b, const void* out) {
   if (m <= 0 || n <= 0 || k <= 0) return set_err(c, MX_EINVAL, "matmul sizes must be positive.");
-  if (n % 64) return set_err(c, MX_EINVAL, "matmul n must be a multiple of 64.");
   if (k % 32) return set_err(c, MX_EINVAL, "matmul k must be a multiple of 32.");
   if (!a || !b || !out || !aligned16(a) || !aligned16(b) || !aligned16(out))
     return set_err(c, MX_EINVAL, "matmul buffers must be non-null and 16-byte aligned.");
@@ -743,6 +779,8 @@ const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index)
   static const char* gemv[] = {"gemv_mxfp4_gate_up_swiglu", "gemv_mxfp4_down"};
   static const char* fused[] = {"gemm_q_mxfp4_gate_up_swiglu", "gemm_q_mxfp4_down"};
   static const char* ref[] = {"gemm_q_mxfp4_gate_up_swiglu_half", "gemm_q_mxfp4_down_f32"};
+  static const char* fused_h[] = {"gemm_h_mxfp4_gate_up_swiglu", "gemm_h_mxfp4_down"};
+  static const char* ref_h[] = {"gemm_h_mxfp4_gate_up_swiglu_half", "gemm_h_mxfp4_down_f32"};
   static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
                               "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
   static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down", "w4a4_down_inf"};
@@ -752,6 +790,8 @@ const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index)
     case PATH_GEMV: return index < 2 ? gemv[index] : nullptr;
     case PATH_GEMM_Q: return index < 2 ? fused[index] : nullptr;
     case PATH_REFROW: return index < 2 ? ref[index] : nullptr;
+    case PATH_GEMM_H: return index < 2 ? fused_h[index] : nullptr;
+    case PATH_REFROW_H: return index < 2 ? ref_h[index] : nullptr;
     case PATH_DEQUANT: return index < 7 ? deq[index] : nullptr;
     case PATH_W4A4: return index < 4 ? w4[index] : nullptr;
     case PATH_SCALED: return index < 3 ? sc[index] : nullptr;
@@ -915,7 +955,9 @@ static int build_moe_steps(mx_ctx* c, const mx_mlp_config* cfg, int n_experts, c
   }
   if (!mx::gemm_q_ok(mx::AK_F16, mx::BK_MXFP4, mx::EPI_SWIGLU_F16, most, I, H) ||
       !mx::gemm_q_ok(mx::AK_F16, mx::BK_MXFP4, mx::EPI_STORE_F16, most, H, I))
-    return set_err(c, MX_EINVAL, "MoE experts with more than 16 tokens need hidden and intermediate %% 64 == 0.");
+    return set_err(c, MX_EINVAL,
+                   "MoE needs hidden and intermediate %% 64 == 0 (%% 128 for the decode GEMV of experts with "
+                   "at most 16 tokens).");
   mx::QGemmArgs gu{x, nullptr, wg, sg, wu, su, mid, nullptr, most, I, H, 0};
   mx::QGemmArgs dn{mid, nullptr, wd, sd, nullptr, nullptr, out, nullptr, most, H, I, 0};
   steps.push_back({"moe_gemm_q_gate_up_swiglu",
@@ -1012,15 +1054,15 @@ static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const 
     return MX_OK;
   }
   const size_t mid_b = align_up((size_t)T * I * 2, 256);
-  const size_t qws_b = std::max(mx::gemm_q_ws_bytes(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, T, I, H),
-                                mx::gemm_q_ws_bytes(mx::AK_F16, bk, mx::EPI_STORE_F16, T, H, I));
+  const size_t qws_b = std::max(q_ws(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, T, I, H),
+                                q_ws(mx::AK_F16, bk, mx::EPI_STORE_F16, T, H, I));
   if (int rc = ensure_ws(c, mid_b + qws_b)) return rc;
   uint16_t* mid = static_cast<uint16_t*>(c->ws);
   void* qws = static_cast<uint8_t*>(c->ws) + mid_b;
   mx::QGemmArgs gu{x, nullptr, w->gate.data, w->gate.scales, w->up.data, w->up.scales, mid, qws, T, I, H, 0};
   mx::QGemmArgs dn{mid, nullptr, w->down.data, w->down.scales, nullptr, nullptr, out, qws, T, H, I, 0};
-  steps.push_back({"gemm_q_fmt_gate_up_swiglu", [=] { return mx::launch_gemm_q(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, gu, st); }});
-  steps.push_back({"gemm_q_fmt_down", [=] { return mx::launch_gemm_q(mx::AK_F16, bk, mx::EPI_STORE_F16, dn, st); }});
+  steps.push_back({"gemm_q_fmt_gate_up_swiglu", [=] { return launch_mlp_gemm(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, gu, st); }});
+  steps.push_back({"gemm_q_fmt_down", [=] { return launch_mlp_gemm(mx::AK_F16, bk, mx::EPI_STORE_F16, dn, st); }});
   return MX_OK;
 }
 

@@ -39,11 +39,12 @@ struct BChunk {  // one thread's slice of a weight tile: row r, 8 k values
 };
 
 // Load this thread's 8-element slice (row r = tid/4, k offset 8*(tid%4)) of
-// weight tile rows [n0, n0+64), k block kb.
+// weight tile rows [n0, n0+64), k block kb.  Rows past the last one (n not
+// a multiple of the tile) re-read row n-1: their columns are never stored.
 template <int BKIND>
 __device__ __forceinline__ void load_b(const void* __restrict__ b, const void* __restrict__ s,
-                                       int n0, int kb, int k, int tid, BChunk<BKIND>& out) {
-  const int r = n0 + (tid >> 2), q = tid & 3;
+                                       int n0, int kb, int n, int k, int tid, BChunk<BKIND>& out) {
+  const int r = min(n0 + (tid >> 2), n - 1), q = tid & 3;
   if (BKIND == BK_F16) {
     const uint16_t* p = reinterpret_cast<const uint16_t*>(b) + (size_t)r * k + kb * 32 + q * 8;
     out.raw = *reinterpret_cast<const uint4*>(p);
@@ -147,8 +148,8 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
     }                                                                                      \
   }
 #define MX_LOAD_B(kb)                                                                      \
-  load_b<BKIND>(g.b0, g.s0, n0, (kb), K, tid, breg[0]);                                   \
-  if (NB == 2) load_b<BKIND>(g.b1, g.s1, n0, (kb), K, tid, breg[NB - 1]);
+  load_b<BKIND>(g.b0, g.s0, n0, (kb), g.n, K, tid, breg[0]);                              \
+  if (NB == 2) load_b<BKIND>(g.b1, g.s1, n0, (kb), g.n, K, tid, breg[NB - 1]);
 #define MX_STORE_B(buf)                                                                    \
   _Pragma("unroll") for (int j = 0; j < NB; j++)                                           \
     *reinterpret_cast<uint4*>(&Bs[buf][(j * kBN + (tid >> 2)) * kLdsRow + (tid & 3) * 8]) = \
@@ -197,8 +198,9 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
     __syncthreads();
   }
 
-  // Epilogue.
+  // Epilogue.  Columns past n (the tail tile) are not stored.
   const int col = n0 + wn * 32 + (lane & 31);
+  if (col >= g.n) return;
   float rs0 = 1.0f, rs1 = 1.0f;
   if (BKIND == BK_E4M3 || BKIND == BK_E5M2 || BKIND == BK_INT8) {
     rs0 = reinterpret_cast<const float*>(g.s0)[col];
@@ -239,12 +241,13 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
 template <int BKIND, int EPI, int A_F32>
 static hipError_t launch_bm(const GemmArgs& g, hipStream_t st) {
   // 128-row tiles when they give at least one workgroup per CU, else 64.
-  const int tiles128 = ((g.m + 127) / 128) * (g.n / kBN);
+  const int tiles_n = (g.n + kBN - 1) / kBN;
+  const int tiles128 = ((g.m + 127) / 128) * tiles_n;
   if (g.m > 64 && tiles128 >= 256) {
-    dim3 grid(g.n / kBN, (g.m + 127) / 128);
+    dim3 grid(tiles_n, (g.m + 127) / 128);
     hipLaunchKernelGGL((k_gemm_h<BKIND, EPI, A_F32, 128>), grid, dim3(256), 0, st, g);
   } else {
-    dim3 grid(g.n / kBN, (g.m + 63) / 64);
+    dim3 grid(tiles_n, (g.m + 63) / 64);
     hipLaunchKernelGGL((k_gemm_h<BKIND, EPI, A_F32, 64>), grid, dim3(256), 0, st, g);
   }
   return hipGetLastError();
@@ -266,8 +269,10 @@ static hipError_t launch_epi(int epi, const GemmArgs& g, hipStream_t st) {
   return hipErrorInvalidValue;
 }
 
-// Preconditions (checked by the caller): n % 64 == 0, k % 32 == 0, m > 0;
-// SwiGLU epilogues take f16 activations.
+// Preconditions (checked by the caller): n >= 1, k % 32 == 0, m > 0;
+// SwiGLU epilogues take f16 activations.  Any n works (the tail tile's rows
+// past n re-read row n-1 and are not stored), as the reference's matmul
+// tiles guard column < n (MXFP4Kernels.metal:98).
 hipError_t launch_gemm_h(int bkind, int epi, const GemmArgs& g, hipStream_t st) {
   switch (bkind) {
     case BK_F16: return launch_epi<BK_F16>(epi, g, st);

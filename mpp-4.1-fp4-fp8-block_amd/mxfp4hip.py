@@ -372,6 +372,14 @@ class Device:
 
 
 # ---- host helpers (no GPU needed) -------------------------------------------
+def mlp_kernel_name(variant: int, tokens: int, hidden: int, inter: int, index: int):
+    """Name of kernel `index` of the forward `variant` runs at this shape
+    (mx_mlp_kernel_name; host logic, no device); None past the last one."""
+    cfg = MlpConfig(tokens, hidden, inter)
+    name = load().mx_mlp_kernel_name(variant, ctypes.byref(cfg), index)
+    return None if name is None else name.decode()
+
+
 def lcg_bytes(seed: int, count: int) -> np.ndarray:
     out = np.empty(count, np.uint8)
     load().mx_lcg_bytes(seed, count, _np_ptr(out))

@@ -62,3 +62,16 @@ def test_checksums_match_oracle():
     h = a.astype(np.float16)
     assert M.checksum_f16raw(h) == O.checksum_f16raw(h)
     assert M.checksum_f32(a[:10])[1] == 10       # step = max(1, count/32)
+
+
+def test_kernel_names_follow_the_shape():
+    """The per-kernel names report the kernel each shape runs (host logic of
+    the library, no device): the decode GEMV for <= 16 tokens at % 128, the
+    64-K-stage family at % 64, the K-step-32 kernel at % 32 only."""
+    assert M.mlp_kernel_name(M.MLP_FUSED, 8, 256, 512, 0) == "gemv_mxfp4_gate_up_swiglu"
+    assert M.mlp_kernel_name(M.MLP_FUSED, 8, 192, 320, 0) == "gemm_q_mxfp4_gate_up_swiglu"
+    assert M.mlp_kernel_name(M.MLP_FUSED, 5, 96, 160, 0) == "gemm_h_mxfp4_gate_up_swiglu"
+    assert M.mlp_kernel_name(M.MLP_FUSED, 40, 1056, 2080, 1) == "gemm_h_mxfp4_down"
+    assert M.mlp_kernel_name(M.MLP_REFROW, 5, 96, 160, 1) == "gemm_h_mxfp4_down_f32"
+    assert M.mlp_kernel_name(M.MLP_REFROW, 128, 1024, 4096, 0) == "gemm_q_mxfp4_gate_up_swiglu_half"
+    assert M.mlp_kernel_name(M.MLP_FUSED, 5, 96, 160, 2) is None
