@@ -2,10 +2,13 @@
 
 Workload (the decode-shaped MLP the north star's
 HBM target is quoted on): tokens=1, hidden=7168, intermediate=2048, x ~ f16
-N(0,1), weights N(0,0.02) quantized to MXFP4 (E2M1 + E8M0 per 32 K), 24
-distinct weight sets rotated inside the timed loop (2.2x the 256 MB
-last-level cache, as for MoE experts).  One step = one full MLP forward
-down(silu(gate(x)) * up(x)).
+N(0,1), weights N(0,0.02) quantized to MXFP4 (E2M1 + E8M0 per 32 K), 77
+distinct weight sets (1.8 GB) rotated inside the timed loop, as for MoE
+experts.  Every configuration takes enough sets that a pass of one kernel
+over one matrix per set streams at least 600 MB (over 2x the 256 MB
+last-level cache); the sets the timed steps do not use run just before the
+timed region, so the timed steps read from HBM.  One step = one full MLP
+forward down(silu(gate(x)) * up(x)).
 
 Secondary measurements (configs 0, 1 with T=8, 2, 3 and 4, and MoE grouped
 experts at the C1 and C2 expert shapes) are reported in
@@ -59,27 +62,52 @@ def roofline_block(bound, work, us, peak_key, kernel):
             "peak_dtype": peak_key, "frac": round(rate / peak, 4), "kernel": kernel, "kernel_us": round(us, 3)}
 
 
-def kernel_work(name, T, H, I):
+# The step kernels of the library's MLP forwards (mx_mlp_kernel_name /
+# mx_fmt_mlp_kernel_name) that a roofline may be taken on, by what bounds
+# them.  Anything else (quantize / split prologues, the byte-255 fix-up
+# passes, the standalone SwiGLU) is never the roofline kernel.
+GEMM_GATE_UP = {"gemm_q_mxfp4_gate_up_swiglu", "gemm_q_mxfp4_gate_up_swiglu_half", "gemm_h_mxfp4_gate_up_swiglu",
+                "gemm_h_mxfp4_gate_up_swiglu_half", "gemm_q_scaled_gate_up_swiglu",
+                "gemm_fp4_gate_up_swiglu_requant"}
+GEMM_ONE = {"gemm_q_mxfp4_down", "gemm_q_mxfp4_down_f32", "gemm_h_mxfp4_down", "gemm_h_mxfp4_down_f32",
+            "gemm_q_scaled_down", "gemm_fp4_down", "gemm_h_h_f_gate", "gemm_h_h_f_up", "gemm_f_h_down"}
+FMT_GATE_UP = {"gemm_q_fmt_gate_up_swiglu", "gemm_h_fmt_gate_up_swiglu", "gemm_q_w8a8_gate_up_swiglu"}
+FMT_DOWN = {"gemm_q_fmt_down", "gemm_h_fmt_down", "gemm_q_w8a8_down"}
+
+
+def fmt_bytes(wfmt, n, k):
+    """Bytes of one format weight matrix [n][k] with its scales."""
+    if wfmt == 4:  # INT4: nibbles + f16 scale per 32
+        return n * k // 2 + n * (k // 32) * 2
+    return n * k + n * 4  # 8-bit codes + f32 row scale
+
+
+def kernel_work(name, T, H, I, wfmt=0):
     """(bound, algorithmic flops or bytes) of one step kernel of an MLP row,
-    from its name in the library's kernel table."""
-    if name.startswith("gemv_"):  # decode GEMV: weights + activations in and out
-        if "gate_up" in name:
-            return "hbm", 2 * mxfp4_bytes(I, H) + T * H * 2 + T * I * 2
+    from its name in the library's kernel table; (None, 0) for kernels that
+    are not a GEMM / GEMV / dequant step."""
+    if name == "gemv_mxfp4_gate_up_swiglu":  # decode GEMV: weights + activations in and out
+        return "hbm", 2 * mxfp4_bytes(I, H) + T * H * 2 + T * I * 2
+    if name == "gemv_mxfp4_down":
         return "hbm", mxfp4_bytes(H, I) + T * I * 2 + T * H * 2
-    if name.startswith("dequant_"):  # MXFP4 in, f16 out
+    if name in ("dequant_gate", "dequant_up", "dequant_down"):  # MXFP4 in, f16 out
         return "hbm", mxfp4_bytes(I, H) + I * H * 2
-    if "gate_up" in name:
+    if name in FMT_GATE_UP:  # format rows are HBM-bound (BASELINE configs[3])
+        return "hbm", 2 * fmt_bytes(wfmt, I, H) + T * H * 2 + T * I * 2
+    if name in FMT_DOWN:
+        return "hbm", fmt_bytes(wfmt, H, I) + T * I * 2 + T * H * 2
+    if name in GEMM_GATE_UP:
         return "mfma", 2 * T * H * 2 * I
-    if name.endswith("_gate") or name.endswith("_up") or name.endswith("_down") or "down" in name:
+    if name in GEMM_ONE:
         return "mfma", 2 * T * H * I
     return None, 0
 
 
-def secondary_roofline(r, T, H, I, peak_key):
+def secondary_roofline(r, T, H, I, peak_key, wfmt=0):
     """Roofline of a secondary row's dominant (longest) GEMM/GEMV kernel."""
     best = None
     for name, us in (r.get("kernel_us") or {}).items():
-        bound, work = kernel_work(name, T, H, I)
+        bound, work = kernel_work(name, T, H, I, wfmt)
         if bound and (best is None or us > best[3]):
             best = (name, bound, work, us)
     if best is None:
@@ -90,6 +118,13 @@ def secondary_roofline(r, T, H, I, peak_key):
 
 def mxfp4_bytes(n, k):
     return n * k // 2 + n * k // 32
+
+
+def sets_for(matrix_bytes, floor=600e6):
+    """Weight sets so that a pass of one kernel over one matrix of each set
+    streams at least `floor` bytes (over 2x the 256 MB last-level cache), so
+    every per-kernel time is measured from HBM."""
+    return int(-(-floor // matrix_bytes))
 
 
 def make_sets(dev, M, T, H, I, n_sets, seed, wfmt=0):
@@ -127,11 +162,10 @@ def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt
     x, sets, bufs = make_sets(dev, M, T, H, I, n_sets, seed, wfmt)
     out = dev.alloc(T * H * 4)
     if wfmt:
-        secs = dev.fmt_mlp_benchmark(wfmt, T, H, I, x, sets, out, warmup=warmup, iterations=iters,
-                                     graph=True)
+        secs, kern = dev.fmt_mlp_benchmark(wfmt, T, H, I, x, sets, out, warmup=warmup, iterations=iters,
+                                           graph=True, per_kernel=True)
         ssecs = dev.fmt_mlp_benchmark(wfmt, T, H, I, x, sets, out, warmup=0, iterations=iters,
                                       graph=False)
-        kern = {}
     else:
         secs, kern = dev.mlp_benchmark(variant, T, H, I, x, sets, out, warmup=warmup,
                                        iterations=iters, graph=True)
@@ -317,7 +351,8 @@ def main():
 
     # ---- headline: config 1, T=1 ------------------------------------------
     T, H, I = 1, 7168, 2048
-    prim, _ = run_config(dev, M, "C1 T=1 fused", M.MLP_FUSED, T, H, I, 24, args.steps,
+    n_sets = sets_for(mxfp4_bytes(H, I))  # 77: the down pass alone streams 600 MB
+    prim, _ = run_config(dev, M, "C1 T=1 fused", M.MLP_FUSED, T, H, I, n_sets, args.steps,
                          args.warmup, seed=1, cpu=None if args.no_cpu else T,
                          cpu_flop_cap=4e11)  # about 12 s of host work for the headline sample
     us = prim["us_per_iter"]
@@ -340,8 +375,8 @@ def main():
         "us_per_iter": us, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic",
         "config": {"workload": "BASELINE configs[1] decode MLP, tokens=1 hidden=7168 "
-                               "intermediate=2048, MXFP4 weights, 24 rotated weight sets",
-                   "tokens": T, "hidden": H, "intermediate": I, "weight_sets": 24,
+                               f"intermediate=2048, MXFP4 weights, {n_sets} rotated weight sets",
+                   "tokens": T, "hidden": H, "intermediate": I, "weight_sets": n_sets,
                    "variant": "decode GEMV, two launches (gate/up + SwiGLU, then down), split-K "
                               "workgroups, in-register FP4 decode, fp16 MFMA"},
         "mlp_hbm_gbps": round(mlp_bytes / (us * 1e-6) / 1e9, 1),
@@ -356,14 +391,15 @@ def main():
         only = set(t for t in args.only.split(",") if t)
         want = lambda tag, variant="": not only or tag in only or f"{tag}_{variant}" in only
         if want("c1_t8"):
-            r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, 24, 200, 10, seed=2, cpu=cpu and 8)
+            r, _ = run_config(dev, M, "C1 T=8", M.MLP_FUSED, 8, 7168, 2048, sets_for(mxfp4_bytes(7168, 2048)),
+                              200, 10, seed=2, cpu=cpu and 8)
             b = 3 * mxfp4_bytes(2048, 7168) + 2 * 8 * 7168 * 2
             r["hbm_frac"] = round(b / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
             r["roofline"] = secondary_roofline(r, 8, 7168, 2048, "f16")
             sec["c1_t8_fused"] = r
         if want("c4"):
-            r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, 1, 10, 2, seed=4,
-                              cpu=cpu and 64)
+            r, _ = run_config(dev, M, "C4 W4A4", M.MLP_W4A4, 4096, 8192, 28672, sets_for(mxfp4_bytes(8192, 28672)),
+                              10, 2, seed=4, cpu=cpu and 64)
             r["fp4_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["fp4"], 4)
             r["roofline"] = secondary_roofline(r, 4096, 8192, 28672, "fp4")
             sec["c4_w4a4"] = r
@@ -371,8 +407,8 @@ def main():
                        (M.MLP_SCALED, "scaled")):
             if not want("c0", tag):
                 continue
-            r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, 24, 100, 10, seed=5,
-                              cpu=cpu and tag == "fused" and 128)
+            r, _ = run_config(dev, M, f"C0 {tag}", v, 128, 1024, 4096, sets_for(mxfp4_bytes(1024, 4096)), 100,
+                              10, seed=5, cpu=cpu and tag == "fused" and 128)
             if v == M.MLP_DEQUANT:
                 r["note"] = DEQUANT_NOTE
             r["roofline"] = secondary_roofline(r, 128, 1024, 4096, "fp4" if tag == "w4a4" else "f16")
@@ -383,8 +419,8 @@ def main():
         for v, tag in ((M.MLP_FUSED, "fused"), (M.MLP_DEQUANT, "dequant"), (M.MLP_SCALED, "scaled")):
             if not want("c2", tag):
                 continue
-            r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, 24, 100, 10, seed=6,
-                              cpu=cpu and tag == "fused" and 512)
+            r, _ = run_config(dev, M, f"C2 {tag}", v, 512, 7168, 2048, sets_for(mxfp4_bytes(7168, 2048)), 100,
+                              10, seed=6, cpu=cpu and tag == "fused" and 512)
             r["f16_mfma_frac"] = round(r["tflops"] * 1e12 / PEAK["f16"], 4)
             if v == M.MLP_DEQUANT:
                 r["note"] = DEQUANT_NOTE
@@ -394,15 +430,13 @@ def main():
                           (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32"), (M.WFMT_W8A8, "w8a8")):
             if not want("c3", tag):
                 continue
-            wb = 3 * 4096 * 14336 * (0.5 if wfmt == M.WFMT_INT4 else 1)
-            # enough rotated weight sets for > 512 MB per format (2x the 256 MB
-            # last-level cache), so every format streams from HBM
-            n_sets = int(512e6 // wb) + 1
-            r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, n_sets, 40, 4, seed=7,
-                              wfmt=wfmt, cpu=cpu and 128)
+            fb = 4 if wfmt == M.WFMT_INT4 else 1  # fmt_bytes' format code (INT4 or 8-bit)
+            wb = 3 * fmt_bytes(fb, 14336, 4096)
+            r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, sets_for(fmt_bytes(fb, 4096, 14336)),
+                              40, 4, seed=7, wfmt=wfmt, cpu=cpu and 128)
             r["hbm_frac"] = round(wb / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
-            # no per-kernel split for the format rows: the whole MLP's weight bytes
-            r["roofline"] = roofline_block("hbm", wb, r["us_per_iter"], None, "whole MLP (weights)")
+            # the longest format GEMM against HBM (weights + activations per launch)
+            r["roofline"] = secondary_roofline(r, 128, 4096, 14336, None, wfmt=fb)
             sec[f"c3_{tag}"] = r
         if want("moe"):
             # MoE grouped launches at the C1 / C2 expert shapes: 64 experts x 4

@@ -226,8 +226,9 @@ int mx_mlp_forward_noalloc(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, c
  * (the reference likewise encodes all iterations into one command buffer,
  * main.swift:2062-2117); 0 launches them one by one.
  * seconds_out: total timed seconds.  kernel_us_out (optional, length
- * >= 8): average device time per iteration of each kernel of the forward, in
- * launch order, from events around each launch in a second timed pass;
+ * >= 8): average device time per launch of each kernel of the forward, in
+ * launch order, each from a timed pass of that kernel alone over the same
+ * rotation (max(iterations, n_sets) launches, so every set is streamed);
  * n_kernels_out: how many were written. */
 int mx_mlp_benchmark(mx_ctx* ctx, int variant, const mx_mlp_config* cfg, const void* x,
                      const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
@@ -285,9 +286,15 @@ int mx_fmt_quantize(mx_ctx* ctx, int wfmt, const float* w, int rows, int k, void
  * hidden and intermediate % 32; W8A8 % 128. */
 int mx_fmt_mlp_forward(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,
                        const mx_mlp_weights* w, void* out);
+/* Timed loop of the format rows, as mx_mlp_benchmark (kernel_us_out and
+ * n_kernels_out optional, per kernel of the forward in launch order). */
 int mx_fmt_mlp_benchmark(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,
                          const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
-                         int iterations, int use_graph, double* seconds_out);
+                         int iterations, int use_graph, double* seconds_out, double* kernel_us_out,
+                         int* n_kernels_out);
+/* Name of kernel `index` of the format forward at shape `cfg`; NULL past the
+ * last kernel. */
+const char* mx_fmt_mlp_kernel_name(int wfmt, const mx_mlp_config* cfg, int index);
 
 /* ---- synthetic data (main.swift:2785-2842) ---------------------------------- */
 /* Seeded N(mean, std) on the device (f32 or f16). */

@@ -819,7 +819,10 @@ static int capture_graph(mx_ctx* c, const std::vector<std::vector<Step>>& sets, 
 }
 
 // Time `iterations` passes over `sets` (set i % n_sets on pass i) between two
-// events: replayed from one captured graph, or launched one by one.
+// events: replayed from one captured graph, or launched one by one.  When
+// there are more sets than passes, the sets the timed passes do not use run
+// once (untimed) just before the timed region, so that what the timed passes
+// read was evicted from the last-level cache by at least that many bytes.
 static int time_passes(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int iterations,
                        int use_graph, double* seconds) {
   const int ns = (int)sets.size();
@@ -830,6 +833,12 @@ static int time_passes(mx_ctx* c, const std::vector<std::vector<Step>>& sets, in
     if (hipGraphLaunch(gexec, c->stream) != hipSuccess) {
       (void)hipGraphExecDestroy(gexec);
       return set_err(c, MX_EGPU, "graph launch failed");
+    }
+  }
+  for (int i = iterations; i < ns; i++) {
+    if (int rc = run_steps(c, sets[(size_t)i])) {
+      if (gexec) (void)hipGraphExecDestroy(gexec);
+      return rc;
     }
   }
   hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -871,17 +880,20 @@ static int bench_loop(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int
   if (int rc = time_passes(c, sets, iterations, use_graph, &secs)) return rc;
   if (seconds_out) *seconds_out = secs;
   if (kernel_us_out || n_kernels_out) {
-    // Per kernel: the same number of back-to-back launches of that kernel
-    // alone (same weight-set rotation, same graph / stream mode), so the
-    // average is the kernel's own duration, as a kernel trace reports it.
+    // Per kernel: back-to-back launches of that kernel alone (same weight-
+    // set rotation, same graph / stream mode), so the average is the
+    // kernel's own duration, as a kernel trace reports it.  At least one
+    // launch per weight set, so that a pass streams every set once whatever
+    // `iterations` is (the caller sizes the sets past the last-level cache).
     const int nk = (int)sets[0].size();
+    const int kiters = std::max(iterations, ns);
     if (n_kernels_out) *n_kernels_out = nk > 8 ? 8 : nk;
     for (int k = 0; k < nk && k < 8; k++) {
       std::vector<std::vector<Step>> one((size_t)ns);
       for (int i = 0; i < ns; i++) one[(size_t)i].push_back(sets[(size_t)i][(size_t)k]);
       double ks = 0.0;
-      if (int rc = time_passes(c, one, iterations, use_graph, &ks)) return rc;
-      if (kernel_us_out) kernel_us_out[k] = ks * 1e6 / iterations;
+      if (int rc = time_passes(c, one, kiters, use_graph, &ks)) return rc;
+      if (kernel_us_out) kernel_us_out[k] = ks * 1e6 / kiters;
     }
   }
   return MX_OK;
@@ -1061,8 +1073,10 @@ static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const 
   void* qws = static_cast<uint8_t*>(c->ws) + mid_b;
   mx::QGemmArgs gu{x, nullptr, w->gate.data, w->gate.scales, w->up.data, w->up.scales, mid, qws, T, I, H, 0};
   mx::QGemmArgs dn{mid, nullptr, w->down.data, w->down.scales, nullptr, nullptr, out, qws, T, H, I, 0};
-  steps.push_back({"gemm_q_fmt_gate_up_swiglu", [=] { return launch_mlp_gemm(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, gu, st); }});
-  steps.push_back({"gemm_q_fmt_down", [=] { return launch_mlp_gemm(mx::AK_F16, bk, mx::EPI_STORE_F16, dn, st); }});
+  steps.push_back({mx_fmt_mlp_kernel_name(wfmt, cfg, 0),
+                   [=] { return launch_mlp_gemm(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, gu, st); }});
+  steps.push_back({mx_fmt_mlp_kernel_name(wfmt, cfg, 1),
+                   [=] { return launch_mlp_gemm(mx::AK_F16, bk, mx::EPI_STORE_F16, dn, st); }});
   return MX_OK;
 }
 
@@ -1076,13 +1090,29 @@ int mx_fmt_mlp_forward(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const void
 
 int mx_fmt_mlp_benchmark(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const void* x,
                          const mx_mlp_weights* sets, int n_sets, void* out, int warmup,
-                         int iterations, int use_graph, double* seconds_out) {
+                         int iterations, int use_graph, double* seconds_out, double* kernel_us_out,
+                         int* n_kernels_out) {
   if (!c) return MX_EINVAL;
   if (!sets || n_sets <= 0) return set_err(c, MX_EINVAL, "benchmark needs at least one weight set.");
   std::vector<std::vector<Step>> all((size_t)n_sets);
   for (int i = 0; i < n_sets; i++)
     if (int rc = build_fmt_steps(c, wfmt, cfg, x, &sets[i], out, all[i])) return rc;
-  return bench_loop(c, all, warmup, iterations, use_graph, seconds_out, nullptr, nullptr);
+  return bench_loop(c, all, warmup, iterations, use_graph, seconds_out, kernel_us_out, n_kernels_out);
+}
+
+const char* mx_fmt_mlp_kernel_name(int wfmt, const mx_mlp_config* cfg, int index) {
+  static const char* w8a8[] = {"quant_x_int8", "gemm_q_w8a8_gate_up_swiglu", "quant_mid_int8", "gemm_q_w8a8_down"};
+  static const char* q[] = {"gemm_q_fmt_gate_up_swiglu", "gemm_q_fmt_down"};
+  static const char* h[] = {"gemm_h_fmt_gate_up_swiglu", "gemm_h_fmt_down"};
+  if (index < 0 || !cfg || wfmt < MX_WFMT_FP8_E4M3 || wfmt > MX_WFMT_W8A8) return nullptr;
+  if (wfmt == MX_WFMT_W8A8) return index < 4 ? w8a8[index] : nullptr;
+  if (index >= 2) return nullptr;
+  const int bk = wfmt == MX_WFMT_FP8_E4M3 ? mx::BK_E4M3 : wfmt == MX_WFMT_FP8_E5M2 ? mx::BK_E5M2
+                 : wfmt == MX_WFMT_INT8 ? mx::BK_INT8 : mx::BK_INT4G32;
+  const int T = cfg->tokens, H = cfg->hidden, I = cfg->intermediate;
+  const bool on_q = index == 0 ? mx::gemm_q_ok(mx::AK_F16, bk, mx::EPI_SWIGLU_F16, T, I, H)
+                               : mx::gemm_q_ok(mx::AK_F16, bk, mx::EPI_STORE_F16, T, H, I);
+  return on_q ? q[index] : h[index];
 }
 
 // ---- synthetic data ------------------------------------------------------------------

@@ -238,7 +238,9 @@ void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long i
     rows.push_back(std::move(r));
   };
 
-  if (H % 64 == 0 && I % 64 == 0) {
+  // MXFP4 rows run whenever hidden and intermediate are multiples of 32, as
+  // the reference's (main.swift:1043).
+  if (H % 32 == 0 && I % 32 == 0) {
     const uint8_t pattern[] = {124, 125, 126, 127, 127, 128, 128, 129, 130};
     const uint32_t data_seeds[3] = {0xabcd1357u, 0x2468bdf0u, 0x0badcafeu};
     const uint32_t scale_seeds[3] = {0x7777ddddu, 0x8888eeeeu, 0x9999ffffu};
@@ -273,6 +275,10 @@ void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long i
         std::printf("  W4A4 row: skipped; hidden and intermediate must be multiples of 128.\n");
         continue;
       }
+      if (v.id == MX_MLP_SCALED && (H % 64 || I % 64)) {
+        std::printf("  scaled-MFMA row: skipped; hidden and intermediate must be multiples of 64.\n");
+        continue;
+      }
       double secs = 0.0;
       // warm-up 1, then `iterations` back to back from one graph (the
       // reference encodes them into one command buffer, :2062-2117)
@@ -280,10 +286,10 @@ void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long i
       record({v.name, secs, iters, checksum(ctx, out.p, T * H, v.f16_out)});
     }
   } else {
-    std::printf("  MXFP4 rows: skipped; hidden and intermediate must be multiples of 64.\n");
+    std::printf("  MXFP4 rows: skipped; hidden and intermediate must be multiples of 32.\n");
   }
 
-  if (H % 64 == 0 && I % 64 == 0) {
+  if (H % 32 == 0 && I % 32 == 0) {
     struct Fmt {
       int id;
       const char* name;
@@ -316,7 +322,7 @@ void run_mlp_benchmark(mx_ctx* ctx, long tokens, long hidden, long inter, long i
       }
       const mx_mlp_weights w{{q0.p, s0.p}, {q1.p, s1.p}, {q2.p, s2.p}};
       double secs = 0.0;
-      check(ctx, mx_fmt_mlp_benchmark(ctx, f.id, &cfg, x.p, &w, 1, out.p, 1, iters, 1, &secs));
+      check(ctx, mx_fmt_mlp_benchmark(ctx, f.id, &cfg, x.p, &w, 1, out.p, 1, iters, 1, &secs, nullptr, nullptr));
       record({f.name, secs, iters, checksum(ctx, out.p, T * H, true)});
     }
   }

@@ -30,7 +30,7 @@ EXPORTS = [
     "mx_mlp_benchmark", "mx_mlp_kernel_name", "mx_mlp_forward_noalloc", "mx_moe_forward", "mx_moe_benchmark",
     "mx_safetensors_find", "mx_load_mxfp4",
     "mx_fmt_quantize", "mx_fmt_mlp_forward",
-    "mx_fmt_mlp_benchmark", "mx_fill_normal", "mx_lcg_bytes", "mx_lcg_pattern", "mx_lcg_half",
+    "mx_fmt_mlp_benchmark", "mx_fmt_mlp_kernel_name", "mx_fill_normal", "mx_lcg_bytes", "mx_lcg_pattern", "mx_lcg_half",
     "mx_lcg_int8", "mx_checksum_f32", "mx_checksum_i32", "mx_checksum_f16raw",
 ]
 
@@ -126,7 +126,8 @@ def load() -> ctypes.CDLL:
         "mx_fmt_quantize": (_int, [_vp, _int, _vp, _int, _int, _vp, _vp]),
         "mx_fmt_mlp_forward": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _vp]),
         "mx_fmt_mlp_benchmark": (_int, [_vp, _int, P(MlpConfig), _vp, P(MlpWeights), _int, _vp,
-                                        _int, _int, _int, P(ctypes.c_double)]),
+                                        _int, _int, _int, P(ctypes.c_double), _vp, _vp]),
+        "mx_fmt_mlp_kernel_name": (ctypes.c_char_p, [_int, ctypes.c_void_p, _int]),
         "mx_fill_normal": (_int, [_vp, _vp, _int, _sz, _u64, _f, _f]),
         "mx_lcg_bytes": (None, [_u32, _sz, _vp]),
         "mx_lcg_pattern": (None, [_u32, _sz, _vp, _int, _vp]),
@@ -361,14 +362,23 @@ class Device:
                                               ctypes.byref(w), out.p))
 
     def fmt_mlp_benchmark(self, wfmt, tokens, hidden, inter, x: DevBuf, sets, out: DevBuf,
-                          warmup=1, iterations=20, graph=True):
+                          warmup=1, iterations=20, graph=True, per_kernel=False):
+        """Seconds for `iterations` forwards; with per_kernel, also
+        {kernel name: us per launch} (mx_fmt_mlp_benchmark)."""
         cfg = MlpConfig(tokens, hidden, inter)
         arr = (MlpWeights * len(sets))(*sets)
         secs = ctypes.c_double()
+        kus = (ctypes.c_double * 8)()
+        nk = ctypes.c_int(0)
         self._check(load().mx_fmt_mlp_benchmark(self.ctx, wfmt, ctypes.byref(cfg), x.p, arr,
                                                 len(sets), out.p, warmup, iterations,
-                                                1 if graph else 0, ctypes.byref(secs)))
-        return secs.value
+                                                1 if graph else 0, ctypes.byref(secs),
+                                                kus if per_kernel else None,
+                                                ctypes.byref(nk) if per_kernel else None))
+        if not per_kernel:
+            return secs.value
+        names = [load().mx_fmt_mlp_kernel_name(wfmt, ctypes.byref(cfg), i).decode() for i in range(nk.value)]
+        return secs.value, dict(zip(names, list(kus)[:nk.value]))
 
 
 # ---- host helpers (no GPU needed) -------------------------------------------
