@@ -91,8 +91,14 @@ def test_mxfp4_matmul_any_n(dev, m, n, k):
         dev.mxfp4_matmul(da, M.DT_F16, dq, dc, c_dtype, m, n, k, ds)
         got = dev.download(dc, npdt, (m, n))
         assert (dev.download(dc.offset(end), np.uint32, (16,)) == 0x7E7E7E7E).all()
-        check(got, ref, f"matmul {m}x{n}x{k} c={c_dtype}", tol=1e-3 if c_dtype == M.DT_F32 else 3e-3,
-              cos_min=0.99999)
+        if c_dtype == M.DT_F32:
+            check(got, ref, f"matmul {m}x{n}x{k} c=f32", tol=1e-3, cos_min=0.99999)
+        else:
+            # f16 C: one rounding of the f32 sum, so within one f16 step of
+            # each element (2^-10 relative) plus the f32 accumulation error
+            err = np.abs(got.astype(np.float64) - ref)
+            rms = np.sqrt((ref ** 2).mean())
+            assert (err <= 2.0 ** -10 * np.abs(ref) + 1e-4 * rms).all(), (m, n, k, (err / rms).max())
         dc.free()
     for b in (da, dq, ds):
         b.free()
