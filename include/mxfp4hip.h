@@ -71,9 +71,11 @@ enum {
    * E8M0 pair per 64 K (relative error <= 2^-8 per value), and
    * v_mfma_scale_f32_32x32x64_f8f6f4 takes the FP4 codes and their E8M0
    * bytes directly, two MFMAs per block.  One more launch (the split of x).
-   * E8M0 byte 255 and non-finite activations give NaN products (the
-   * hardware's reading), where the other variants keep the reference's
-   * +inf scale. */
+   * The MFMA reads E8M0 byte 255 as NaN; the outputs that turns NaN (and
+   * those of non-finite activations) are recomputed in the epilogues with
+   * the reference's +inf scale, so NaN and +-inf land where the reference's
+   * do.  (A non-finite mid is carried as its class: NaN, +-inf, zero or the
+   * sign of a finite value.) */
   MX_MLP_SCALED = 4
 };
 

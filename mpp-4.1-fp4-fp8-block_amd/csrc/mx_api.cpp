@@ -295,7 +295,7 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
     uint8_t* mq = ws + s.mq;
     uint32_t* me = reinterpret_cast<uint32_t*>(ws + s.me);
     void* qws = ws + s.qws;
-    mx::QGemmArgs gu{xq, nullptr, wg, sg, wu, su, mq, qws, T, I, H, 0, xe, me};
+    mx::QGemmArgs gu{xq, nullptr, wg, sg, wu, su, mq, qws, T, I, H, 0, xe, me, static_cast<const uint16_t*>(x)};
     mx::QGemmArgs dn{mq, nullptr, wd, sd, nullptr, nullptr, out, qws, T, H, I, 0, me, nullptr};
     steps.push_back({"split_x_f8x2", [=] {
                        return mx::launch_split_f8x2(static_cast<const uint16_t*>(x), T, H, xq, xe, st);

@@ -114,6 +114,68 @@ __device__ __forceinline__ uint32_t mxfp4_scale_byte(uint32_t amax_bits) {
   return (uint32_t)(s + 127);
 }
 
+// One E4M3 byte -> f32 (0x7f / 0xff NaN, no infinities).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(byte & 255u, 1.0f, false)[0];
+}
+
+// ---------------------------------------------------------------------------
+// Exact (reference-semantics) recomputation of single outputs whose tiled
+// result is NaN.  The scaled MFMA reads E8M0 byte 255 as NaN where the
+// reference decodes it as +inf (MXFP4Kernels.metal:26-29, bits << 23), and
+// its F8X2 activations cannot hold an infinity.  These scalar loops dequantize
+// like the reference (w = FP4 value * 2^(s - 127), byte 255 -> +inf, byte 0
+// -> 0) and accumulate in f32 in K order, so IEEE arithmetic reproduces the
+// reference's non-finite results: x * inf = +-inf, 0 * inf = NaN, inf - inf =
+// NaN.  Finite parts are as accurate as any f32 dot product.
+
+// sum_k x[k] * W[k] for one f16 activation row and one MXFP4 weight row.
+__device__ inline float ref_dot_f16_mxfp4(const uint16_t* x, const uint8_t* w, const uint8_t* s, int K) {
+  float acc = 0.0f;
+  for (int kb = 0; kb < K / 32; kb++) {
+    const float sc = e8m0_to_float(s[kb]);
+    for (int j = 0; j < 16; j++) {
+      const v2f c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[kb * 16 + j], 1.0f, 0);
+      acc += f16_bits_to_f32(x[kb * 32 + 2 * j]) * (c[0] * sc);
+      acc += f16_bits_to_f32(x[kb * 32 + 2 * j + 1]) * (c[1] * sc);
+    }
+  }
+  return acc;
+}
+
+// Value k of row `row` of an F8X2 matrix (layout in mx_internal.h; K % 64 ==
+// 0, M rows): t1 s1 + t2 s2, or for a group with scale byte 255 the class its
+// first term carries (NaN, +-inf, 0, or +-1 for a finite non-zero value).
+__device__ inline float f8x2_ref_value(const uint8_t* data, const uint32_t* e8, int M, int K, int row, int k) {
+  const int gi = k >> 6, kk = k & 63, q = kk >> 4;
+  const int pos = (kk & 15) + 16 * (q == 1 ? 2 : q == 2 ? 1 : q);
+  const uint8_t* grp = data + ((size_t)row * (K / 64) + gi) * 128;
+  const uint32_t e = e8[(size_t)gi * M + row], b1 = e & 255u, b2 = (e >> 8) & 255u;
+  const uint32_t t1 = grp[pos], t2 = grp[64 + pos];
+  if (b1 == 255u) {
+    const float sg = (t1 & 0x80u) ? -1.0f : 1.0f;
+    if ((t1 & 0x7fu) == 0x7fu) return __builtin_nanf("");
+    if ((t1 & 0x7fu) == 0x7eu) return sg * __builtin_inff();
+    return (t1 & 0x7fu) ? sg : 0.0f;
+  }
+  return e4m3_to_f32(t1) * e8m0_as_cvt_scale(b1) + e4m3_to_f32(t2) * e8m0_as_cvt_scale(b2);
+}
+
+// sum_k a[row][k] * W[k] for an F8X2 activation row and one MXFP4 weight row.
+__device__ inline float ref_dot_f8x2_mxfp4(const uint8_t* data, const uint32_t* e8, int M, int row,
+                                           const uint8_t* w, const uint8_t* s, int K) {
+  float acc = 0.0f;
+  for (int kb = 0; kb < K / 32; kb++) {
+    const float sc = e8m0_to_float(s[kb]);
+    for (int j = 0; j < 16; j++) {
+      const v2f c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[kb * 16 + j], 1.0f, 0);
+      acc += f8x2_ref_value(data, e8, M, K, row, kb * 32 + 2 * j) * (c[0] * sc);
+      acc += f8x2_ref_value(data, e8, M, K, row, kb * 32 + 2 * j + 1) * (c[1] * sc);
+    }
+  }
+  return acc;
+}
+
 // F8X2 term scale of a group with amax bits `amax_bits` (finite, > 0): the
 // smallest power of two s with amax <= 448 s (the E4M3 maximum, so no code
 // saturates), as an E8M0 byte (clamped at 2^-127).
@@ -131,10 +193,14 @@ __device__ __forceinline__ uint32_t f8x2_scale_byte(uint32_t amax_bits) {
 // k [V j, V j + V) in v.  t1 = RNE_E4M3(v / s1); the residual r = v - t1 s1
 // is exact in f32; t2 = RNE_E4M3(r / s2), each s from its term's group
 // maximum.  A group with a non-finite value gets scale bytes 255 (its
-// products are NaN) and NaN codes; an all-zero group gets bytes 127 and zero
-// codes.  All L lanes must be active (they exchange maxima).  Writes the
-// lane's bytes of both terms into the group's 128 bytes at `grp` and, from
-// lane j = 0, the scale dword at `e8`.
+// products are NaN, which marks every output it feeds) and carries the class
+// of each value in its first term's byte for the exact fix-up of those
+// outputs (f8x2_ref_value): 0x7f NaN, 0x7e +inf, 0xfe -inf, 0x00 zero, 0x38 /
+// 0xb8 a finite non-zero value of that sign (as +-1); the second term is zero.
+// An all-zero group gets bytes 127 and zero codes.  All L lanes must be
+// active (they exchange maxima).  Writes the lane's bytes of both terms into
+// the group's 128 bytes at `grp` and, from lane j = 0, the scale dword at
+// `e8`.
 template <int L>
 __device__ __forceinline__ void f8x2_split_store(const float* v, int j, uint8_t* grp, uint32_t* e8) {
   constexpr int V = 64 / L, D = V / 4;  // values and dwords per lane and term
@@ -149,7 +215,18 @@ __device__ __forceinline__ void f8x2_split_store(const float* v, int j, uint8_t*
   if (am >= 0x7f800000u) {
     b1 = b2 = 255u;
 #pragma unroll
-    for (int d = 0; d < D; d++) t1[d] = t2[d] = 0x7f7f7f7fu;
+    for (int d = 0; d < D; d++) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint32_t u = __builtin_bit_cast(uint32_t, v[4 * d + t]), a = u & 0x7fffffffu;
+        const uint32_t sg = (u >> 24) & 0x80u;
+        const uint32_t code = a > 0x7f800000u ? 0x7fu : a == 0x7f800000u ? (0x7eu | sg) : a ? (0x38u | sg) : 0u;
+        w |= code << (8 * t);
+      }
+      t1[d] = w;
+      t2[d] = 0u;
+    }
   } else {
 #pragma unroll
     for (int d = 0; d < D; d++) t1[d] = t2[d] = 0u;

@@ -776,14 +776,45 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       }
     __syncthreads();
     const int pr = tid >> 1, half = tid & 1, rl = pr & 63;
-    const float* src = reinterpret_cast<const float*>(pr < 64 ? ms0 : ms1);
+    float* src = reinterpret_cast<float*>(pr < 64 ? ms0 : ms1);
     float mv[32];
+    uint32_t nf = 0;  // a non-finite mid value among the lane's 32
 #pragma unroll
     for (int k = 0; k < 32; k++) {
       const int c = 32 * half + k;
       mv[k] = src[rl * 64 + (c ^ (rl & 31))];
+      nf |= (uint32_t)((__builtin_bit_cast(uint32_t, mv[k]) & 0x7fffffffu) >= 0x7f800000u);
     }
     const int row = m0 + pr, grp = n0 / 64;
+    // E8M0 byte 255 in a gate / up scale (NaN in the scaled MFMA, +inf in the
+    // reference) or a non-finite x leaves non-finite mid values: those
+    // channels are recomputed from the f16 activations with the reference's
+    // dequantization (rare; one wave-uniform test).  One rolled loop, results
+    // back through the lane's own LDS slots.
+    if (__builtin_expect(__ballot(nf != 0) != 0, 0)) {
+      if (nf && row < M && g.a_f16) {
+        const uint16_t* xr = g.a_f16 + (size_t)row * K;
+        const uint8_t* wg = reinterpret_cast<const uint8_t*>(g.b0);
+        const uint8_t* wu = reinterpret_cast<const uint8_t*>(g.b1);
+        const uint8_t* sg = reinterpret_cast<const uint8_t*>(g.s0);
+        const uint8_t* su = reinterpret_cast<const uint8_t*>(g.s1);
+#pragma nounroll
+        for (int k = 0; k < 32; k++) {
+          const int c = 32 * half + k, ch = n0 + c;
+          float* p = src + rl * 64 + (c ^ (rl & 31));
+          if ((__builtin_bit_cast(uint32_t, *p) & 0x7fffffffu) >= 0x7f800000u) {
+            const float gv = ref_dot_f16_mxfp4(xr, wg + (size_t)ch * (K / 2), sg + (size_t)ch * (K / 32), K);
+            const float uv = ref_dot_f16_mxfp4(xr, wu + (size_t)ch * (K / 2), su + (size_t)ch * (K / 32), K);
+            *p = (gv / (1.0f + expf(-gv))) * uv;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+          const int c = 32 * half + k;
+          mv[k] = src[rl * 64 + (c ^ (rl & 31))];
+        }
+      }
+    }
     if (row < M)
       f8x2_split_store<2>(mv, half, reinterpret_cast<uint8_t*>(g.c) + (size_t)row * 2 * g.n + (size_t)grp * 128,
                           g.c_e8 + (size_t)grp * M + row);
@@ -839,6 +870,36 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   };
   if (full_tile) epilogue(std::false_type{});
   else epilogue(std::true_type{});
+  if constexpr (AK == AK_F8X2 && !DUAL) {
+    // A NaN output (E8M0 byte 255 in a weight scale: NaN in the scaled MFMA,
+    // +inf in the reference; or a non-finite activation group) is recomputed
+    // with the reference's dequantization (rare; one wave-uniform test).
+    uint64_t nanm = 0;  // bit (i NWB + jj) 16 + v: element is NaN
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int jj = 0; jj < NWB; jj++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const float x0 = acc[i][jj][v];
+          nanm |= (uint64_t)(x0 != x0) << ((i * NWB + jj) * 16 + v);
+        }
+    if (__builtin_expect(__ballot(nanm != 0) != 0, 0)) {
+      const uint8_t* ad = reinterpret_cast<const uint8_t*>(g.a);
+      const uint8_t* wb = reinterpret_cast<const uint8_t*>(g.b0);
+      const uint8_t* sb = reinterpret_cast<const uint8_t*>(g.s0);
+#pragma nounroll
+      for (int e = 0; e < 2 * NWB * 16; e++) {
+        if (!((nanm >> e) & 1u)) continue;
+        const int i = e / (NWB * 16), jj = (e / 16) % NWB, v = e % 16;
+        const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, v);
+        const int col = n0 + b_blk[jj] + r32;
+        if (row >= M) continue;
+        const float r = ref_dot_f8x2_mxfp4(ad, g.a_e8, M, row, wb + (size_t)col * (K / 2), sb + (size_t)col * (K / 32), K);
+        epi_store<EPI>(g.c, (size_t)row * g.n + col, r, 0.0f);
+      }
+    }
+  }
 }
 
 // Split-K reduction + epilogue: four consecutive output elements per thread
@@ -870,6 +931,23 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
     float mv[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) mv[c] = (gs[c] / (1.0f + expf(-gs[c]))) * us[c];
+    // non-finite mid (E8M0 byte 255 in a gate / up scale, or a non-finite x):
+    // recomputed from the f16 activations with the reference's dequantization
+    if (g.a_f16) {
+      const int K = g.k;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if ((__builtin_bit_cast(uint32_t, mv[c]) & 0x7fffffffu) >= 0x7f800000u) {
+          const int ch = grp * 64 + 4 * j + c;
+          const uint16_t* xr = g.a_f16 + (size_t)row * K;
+          const float gv = ref_dot_f16_mxfp4(xr, reinterpret_cast<const uint8_t*>(g.b0) + (size_t)ch * (K / 2),
+                                             reinterpret_cast<const uint8_t*>(g.s0) + (size_t)ch * (K / 32), K);
+          const float uv = ref_dot_f16_mxfp4(xr, reinterpret_cast<const uint8_t*>(g.b1) + (size_t)ch * (K / 2),
+                                             reinterpret_cast<const uint8_t*>(g.s1) + (size_t)ch * (K / 32), K);
+          mv[c] = (gv / (1.0f + expf(-gv))) * uv;
+        }
+      }
+    }
     f8x2_split_store<16>(mv, j, reinterpret_cast<uint8_t*>(g.c) + (size_t)row * 2 * g.n + (size_t)grp * 128,
                          g.c_e8 + (size_t)grp * g.m + row);
     return;
@@ -913,8 +991,16 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
   }
 #pragma unroll
   for (int t = 0; t < 4; t++) {
-    const float x0 = scaled<AK, BK>(sums[0][t], g, reinterpret_cast<const float*>(g.s0), row, col + t);
+    float x0 = scaled<AK, BK>(sums[0][t], g, reinterpret_cast<const float*>(g.s0), row, col + t);
     const float u = DUAL ? scaled<AK, BK>(sums[PL - 1][t], g, reinterpret_cast<const float*>(g.s1), row, col + t) : 0.0f;
+    if (AK == AK_F8X2 && !DUAL && x0 != x0) {
+      // E8M0 byte 255 in a weight scale (NaN in the scaled MFMA, +inf in the
+      // reference) or a non-finite activation group: recomputed with the
+      // reference's dequantization
+      x0 = ref_dot_f8x2_mxfp4(reinterpret_cast<const uint8_t*>(g.a), g.a_e8, g.m, row,
+                              reinterpret_cast<const uint8_t*>(g.b0) + (size_t)(col + t) * (g.k / 2),
+                              reinterpret_cast<const uint8_t*>(g.s0) + (size_t)(col + t) * (g.k / 32), g.k);
+    }
     epi_store<EPI>(g.c, o + t, x0, u);
   }
 }

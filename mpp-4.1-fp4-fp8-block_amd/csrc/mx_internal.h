@@ -101,6 +101,8 @@ struct QGemmArgs {
   int tiles_m;                            // set by the launcher
   const uint32_t* a_e8;                   // AK_F8X2: E8M0 pairs [K/64][M]
   uint32_t* c_e8;                         // EPI_SWIGLU_F8X2: mid E8M0 pairs [N/64][M]
+  const uint16_t* a_f16;                  // EPI_SWIGLU_F8X2: the f16 activations the F8X2
+                                          // ones were split from (exact fix-up of NaN outputs)
 };
 bool gemm_q_ok(int akind, int bkind, int epi, int m, int n, int k);
 size_t gemm_q_ws_bytes(int akind, int bkind, int epi, int m, int n, int k);

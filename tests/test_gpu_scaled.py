@@ -86,26 +86,74 @@ def test_scaled_rejects_bad_shapes(dev):
     d.free()
 
 
-@pytest.mark.parametrize("which", ["down", "gate"])
-def test_scaled_e8m0_255_is_nan(dev, which):
-    """The scaled MFMA reads E8M0 byte 255 as NaN, where the reference's
-    bits << 23 gives +inf.  This variant keeps the hardware reading: every
-    output the reference makes non-finite (NaN or +-inf) is NaN here, and
-    every other output stays within tolerance."""
-    T, H, I = 5, 512, 1024
-    d = MlpData(dev, T, H, I, seed=77)
-    q, s, n, k = d.mats[{"gate": 0, "down": 2}[which]]
-    sc = dev.download(s, np.uint8, (n, k // 32))
-    sc[3, 2] = 255
-    dev.upload(sc, s)
+def _plant(dev, d, which):
+    """Cases the reference (bits << 23: byte 255 = +inf, 0 = 0.0) makes
+    +-inf as well as NaN.  x row 0 is positive and row 1 negative; gate / up
+    rows 96..127 and down row 7 are all code +1.0.
+      gate / up: byte 255 on block 0 of row 96.  Token 0 gets g or u = +inf
+        there, token 1 g = -inf (silu -> NaN) or u = -inf (mid = +inf); the
+        other tokens' mixed signs give NaN.  A token with an infinite mid
+        has +-inf outputs (NaN where a down code is zero).
+      down: byte 255 at (3, 2), on all of row H-1, and at (7, 3), where
+        tokens 0 and 1 meet equal-signed mid values: out[0][7] = +inf.
+    Byte 0 rides along in each plane."""
+    x = dev.download(d.x, np.float16, (d.T, d.H))
+    x[0] = np.abs(x[0]) + np.float16(0.25)
+    x[1] = -(np.abs(x[1]) + np.float16(0.25))
+    dev.upload(x, d.x)
+    for j in (0, 1):
+        q, _, n, k = d.mats[j]
+        codes = dev.download(q, np.uint8, (n, k // 2))
+        codes[96:128, :] = 0x22
+        dev.upload(codes, q)
+    q, _, n, k = d.mats[2]
+    codes = dev.download(q, np.uint8, (n, k // 2))
+    codes[7, :] = 0x22
+    dev.upload(codes, q)
+    q, s_, n, k = d.mats[{"gate": 0, "up": 1, "down": 2}[which]]
+    sc = dev.download(s_, np.uint8, (n, k // 32))
+    if which == "down":
+        sc[3, 2] = 255
+        sc[n - 1, :] = 255
+        sc[7, 3] = 255
+        sc[11, 0] = 0
+    else:
+        sc[96, 0] = 255
+        sc[100, 1] = 0
+    dev.upload(sc, s_)
+
+
+# (64, 512, 256): both GEMMs store from their own epilogue (no K split);
+# C0 (128, 1024, 4096): both split K, so the reduce kernels store.
+@pytest.mark.parametrize("T,H,I", [(64, 512, 256), (128, 1024, 4096)])
+@pytest.mark.parametrize("which", ["gate", "up", "down"])
+def test_scaled_e8m0_endpoints(dev, which, T, H, I):
+    """E8M0 byte 255 is +inf to the reference (bits << 23,
+    MXFP4Kernels.metal:26-29) and NaN to the scaled MFMA.  The outputs it
+    turns NaN are recomputed with the reference's dequantization, so NaN,
+    +inf and -inf land exactly where the oracle's do, and every finite
+    output stays within tolerance."""
+    d = MlpData(dev, T, H, I, seed=177 + T)
+    _plant(dev, d, which)
     got = run(dev, d, M.MLP_SCALED).astype(np.float64)
     ref = oracle(d)
-    nonfin = ~np.isfinite(ref)
-    assert nonfin.any()
-    assert np.isnan(got[nonfin]).all()
-    assert np.isfinite(got[~nonfin]).all()
-    if which == "down":  # output column 3 only
-        assert nonfin.sum() == T
-        rel, cos = O.mlp_error(got[~nonfin], ref[~nonfin])
-        assert rel <= TOL and cos >= COS, (rel, cos)
+    if which == "down":
+        assert np.isposinf(ref[0, 7]), ref[0, 7]
+        assert np.isfinite(ref[:, 8:H - 1]).all()
+    else:  # token 0's mid[96] = +inf: +-inf outputs, NaN at zero down codes
+        assert np.isinf(ref[0]).sum() > H // 2, np.isinf(ref[0]).sum()
+    if which == "up":  # u[1][96] = -inf times silu(g) < 0: mid = +inf
+        assert np.isinf(ref[1]).sum() > H // 2, np.isinf(ref[1]).sum()
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), (which, np.isnan(got).sum(), np.isnan(ref).sum())
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)), which
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref)), which
+    # finite outputs within tolerance, the two planted tokens apart from the
+    # rest: their all-+1 rows give mid values ~50x the others, so their
+    # outputs would set the rms that the other tokens' errors are held to
+    fin = np.isfinite(ref)
+    for rows in (slice(0, 2), slice(2, T)):
+        f = fin[rows]
+        if f.any():
+            rel, cos = O.mlp_error(got[rows][f], ref[rows][f])
+            assert rel <= TOL and cos >= COS, (which, rows, rel, cos)
     d.free()
