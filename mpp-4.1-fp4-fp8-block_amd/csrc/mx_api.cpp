@@ -146,8 +146,11 @@ bool gemv_ok(const mx_mlp_config* cfg) {
 // PATH_GEMM_H: the fused (or reference-row) MLP at shapes the 64-K-stage
 // family does not take (hidden or intermediate % 64 != 0): both GEMMs on the
 // K-step-32 kernel.
+// PATH_W4A4: stage-major scale planes (the 256 x 256 kernels, whose down
+// epilogue recomputes byte-255 outputs itself); PATH_W4A4_REF: the
+// reference-layout kernels plus a separate byte-255 pass.
 enum MlpPath { PATH_GEMV, PATH_GEMM_Q, PATH_REFROW, PATH_DEQUANT, PATH_W4A4, PATH_SCALED, PATH_GEMM_H,
-               PATH_REFROW_H };
+               PATH_REFROW_H, PATH_W4A4_REF };
 
 bool q_shapes(const mx_mlp_config* cfg) { return cfg->hidden % 64 == 0 && cfg->intermediate % 64 == 0; }
 
@@ -157,7 +160,7 @@ MlpPath mlp_path(int variant, const mx_mlp_config* cfg) {
     case MX_MLP_REFROW: return q_shapes(cfg) ? PATH_REFROW : PATH_REFROW_H;
     case MX_MLP_DEQUANT: return PATH_DEQUANT;
     case MX_MLP_SCALED: return PATH_SCALED;
-    default: return PATH_W4A4;
+    default: return mx::w4a4_stage_major_ok((int)cfg->hidden, (int)cfg->intermediate) ? PATH_W4A4 : PATH_W4A4_REF;
   }
 }
 
@@ -341,9 +344,6 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
       steps.push_back({"w4a4_prologue", [=] { return mx::launch_w4a4_prologue(pro, st); }});
       steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
       steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});
-      steps.push_back({"w4a4_down_inf", [=] {
-                         return mx::launch_w4a4_down_inf(wd, sd, mq, ms, 1, T, H, I, static_cast<uint16_t*>(out), st);
-                       }});
     } else {
       mx::Fp4GemmArgs gu{xq, xs, wg, sg, wu, su, mq, ms, T, I, H, 0};
       mx::Fp4GemmArgs dn{mq, ms, wd, sd, nullptr, nullptr, out, nullptr, T, H, I, 0};
@@ -784,6 +784,7 @@ const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index)
   static const char* deq[] = {"dequant_gate", "dequant_up", "dequant_down", "gemm_h_h_f_gate",
                               "gemm_h_h_f_up", "swiglu_float", "gemm_f_h_down"};
   static const char* w4[] = {"w4a4_prologue", "gemm_fp4_gate_up_swiglu_requant", "gemm_fp4_down", "w4a4_down_inf"};
+  // (the stage-major path runs the first three; the reference-layout one all four)
   static const char* sc[] = {"split_x_f8x2", "gemm_q_scaled_gate_up_swiglu", "gemm_q_scaled_down"};
   if (index < 0 || !cfg || variant < MX_MLP_FUSED || variant > MX_MLP_SCALED) return nullptr;
   switch (mlp_path(variant, cfg)) {
@@ -793,7 +794,8 @@ const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index)
     case PATH_GEMM_H: return index < 2 ? fused_h[index] : nullptr;
     case PATH_REFROW_H: return index < 2 ? ref_h[index] : nullptr;
     case PATH_DEQUANT: return index < 7 ? deq[index] : nullptr;
-    case PATH_W4A4: return index < 4 ? w4[index] : nullptr;
+    case PATH_W4A4: return index < 3 ? w4[index] : nullptr;
+    case PATH_W4A4_REF: return index < 4 ? w4[index] : nullptr;
     case PATH_SCALED: return index < 3 ? sc[index] : nullptr;
   }
   return nullptr;

@@ -176,6 +176,33 @@ __device__ inline float ref_dot_f8x2_mxfp4(const uint8_t* data, const uint32_t* 
   return acc;
 }
 
+// E8M0 byte of (row, 32-K block b) in a stage-major scale plane: [K/128]
+// planes of `rows` dwords, each the four bytes of one row's 128-K stage.
+__device__ __forceinline__ uint32_t e8m0_stage_major(const uint8_t* s, size_t rows, int row, int b) {
+  return s[(((size_t)(b >> 2) * rows + row) << 2) + (b & 3)];
+}
+
+// sum_k A[row][k] * W[col][k] with both operands MXFP4 (codes [.][K/2], low
+// nibble = even k; stage-major scale planes of a_rows / w_rows rows), each
+// dequantized as the reference does before the product.
+__device__ inline float ref_dot_mxfp4_mxfp4(const uint8_t* a, const uint8_t* as, size_t a_rows, int row,
+                                           const uint8_t* w, const uint8_t* ws, size_t w_rows, int col, int K) {
+  const uint8_t* ar = a + (size_t)row * (K / 2);
+  const uint8_t* wr = w + (size_t)col * (K / 2);
+  float acc = 0.0f;
+  for (int b = 0; b < K / 32; b++) {
+    const float sa = e8m0_to_float(e8m0_stage_major(as, a_rows, row, b));
+    const float sw = e8m0_to_float(e8m0_stage_major(ws, w_rows, col, b));
+    for (int j = 0; j < 16; j++) {
+      const v2f ca = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(ar[b * 16 + j], 1.0f, 0);
+      const v2f cw = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wr[b * 16 + j], 1.0f, 0);
+      acc += (ca[0] * sa) * (cw[0] * sw);
+      acc += (ca[1] * sa) * (cw[1] * sw);
+    }
+  }
+  return acc;
+}
+
 // F8X2 term scale of a group with amax bits `amax_bits` (finite, > 0): the
 // smallest power of two s with amax <= 448 s (the E4M3 maximum, so no code
 // saturates), as an E8M0 byte (clamped at 2^-127).

@@ -266,6 +266,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
 
   if (!DUAL) {
     uint16_t* c = reinterpret_cast<uint16_t*>(g.c);
+    uint64_t nanm[4] = {0u, 0u, 0u, 0u};  // bit j * 16 + v of word i: element is NaN
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -274,9 +275,26 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
 #pragma unroll
         for (int v = 0; v < 16; v++) {
           const int row = m0 + wm * 128 + i * 32 + acc32_row(lane, v);
-          if (row < M) c[(size_t)row * g.n + col] = f32_to_f16_bits(acc[i][j][v]);
+          const float x0 = acc[i][j][v];
+          nanm[i] |= (uint64_t)(x0 != x0) << (j * 16 + v);
+          if (row < M) c[(size_t)row * g.n + col] = f32_to_f16_bits(x0);
         }
       }
+    // E8M0 byte 255 in a down-weight scale is NaN to the scaled MFMA and
+    // +inf to the reference (MXFP4Kernels.metal:26-29), whose dequantize-
+    // then-accumulate gives +-inf or NaN there: NaN outputs (rare; one
+    // wave-uniform test) are recomputed with the reference's dequantization.
+    if (__builtin_expect(__ballot((nanm[0] | nanm[1] | nanm[2] | nanm[3]) != 0) != 0, 0)) {
+#pragma nounroll
+      for (int e = 0; e < 256; e++) {
+        const int i = e >> 6, j = (e >> 4) & 3, v = e & 15;
+        if (!((nanm[i] >> (j * 16 + v)) & 1u)) continue;
+        const int row = m0 + wm * 128 + i * 32 + acc32_row(lane, v);
+        const int col = nt * 256 + (wn * 4 + j) * 32 + r32;
+        if (row < M)
+          c[(size_t)row * g.n + col] = f32_to_f16_bits(ref_dot_mxfp4_mxfp4(g.a, g.as, Mpad, row, g.b0, g.s0, NB, col, K));
+      }
+    }
     return;
   }
   // mid = silu(gate) * up re-quantized along channels (stage-major scales).
@@ -324,6 +342,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v5(Fp4GemmArgs g) {
 
 // Split-K reduce, plain epilogue: 4 consecutive outputs per thread, the
 // splits summed in order 0, 1, ... in f32, stored as f16.
+// A NaN sum (E8M0 byte 255 in a down-weight scale) is recomputed with the
+// reference's dequantization, as in the unsplit epilogue.
 __global__ __launch_bounds__(256) void k_fp4_reduce_f16(Fp4GemmArgs g) {
   const size_t plane = (size_t)g.m * g.n;
   const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -332,6 +352,12 @@ __global__ __launch_bounds__(256) void k_fp4_reduce_f16(Fp4GemmArgs g) {
   for (int k = 0; k < g.splits; k++) {
     const float4 v = *reinterpret_cast<const float4*>(g.ws + (size_t)k * plane + o);
     s[0] += v.x; s[1] += v.y; s[2] += v.z; s[3] += v.w;
+  }
+  for (int t = 0; t < 4; t++) {
+    if (s[t] != s[t]) {
+      const int row = (int)((o + t) / g.n), col = (int)((o + t) % g.n);
+      s[t] = ref_dot_mxfp4_mxfp4(g.a, g.as, stage_major_rows(g.m), row, g.b0, g.s0, (size_t)g.n, col, g.k);
+    }
   }
   uint2 h;
   h.x = f32_to_f16_bits(s[0]) | ((uint32_t)f32_to_f16_bits(s[1]) << 16);

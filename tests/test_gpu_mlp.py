@@ -431,7 +431,11 @@ def test_e8m0_endpoints_tiled_paths(dev, variant, which):
     d.free()
 
 
-@pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (96, 640, 1152)])
+# (64, 512, 1024): stage-major planes, the down GEMM split over K (its reduce
+# stores); (512, 2048, 512): the unsplit 256-K-stage down GEMM stores;
+# (64, 512, 640): the 128-K-stage down GEMM (K % 512 != 0) stores; (96, 640,
+# 1152): reference-layout planes with the separate byte-255 pass.
+@pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (512, 2048, 512), (64, 512, 640), (96, 640, 1152)])
 @pytest.mark.parametrize("which", ["up", "down"])
 def test_e8m0_endpoints_w4a4(dev, T, H, I, which):
     """W4A4 (both scale layouts): byte 255 in an up scale makes the channel's
