@@ -71,8 +71,9 @@ GEMM_GATE_UP = {"gemm_q_mxfp4_gate_up_swiglu", "gemm_q_mxfp4_gate_up_swiglu_half
                 "gemm_fp4_gate_up_swiglu_requant"}
 GEMM_ONE = {"gemm_q_mxfp4_down", "gemm_q_mxfp4_down_f32", "gemm_h_mxfp4_down", "gemm_h_mxfp4_down_f32",
             "gemm_q_scaled_down", "gemm_fp4_down", "gemm_h_h_f_gate", "gemm_h_h_f_up", "gemm_f_h_down"}
-FMT_GATE_UP = {"gemm_q_fmt_gate_up_swiglu", "gemm_h_fmt_gate_up_swiglu", "gemm_q_w8a8_gate_up_swiglu"}
-FMT_DOWN = {"gemm_q_fmt_down", "gemm_h_fmt_down", "gemm_q_w8a8_down"}
+FMT_GATE_UP = {"gemm_q_fmt_gate_up_swiglu", "gemm_h_fmt_gate_up_swiglu", "gemm_q_w8a8_gate_up_swiglu",
+               "gemm_q_f8x2_fmt_gate_up_swiglu"}
+FMT_DOWN = {"gemm_q_fmt_down", "gemm_h_fmt_down", "gemm_q_w8a8_down", "gemm_q_f8x2_fmt_down"}
 
 
 def fmt_bytes(wfmt, n, k):
@@ -426,14 +427,18 @@ def main():
                 r["note"] = DEQUANT_NOTE
             r["roofline"] = secondary_roofline(r, 512, 7168, 2048, "f16")
             sec[f"c2_{tag}"] = r
+        # the _f8x2 rows: the FP8 weights of the first two rows on the scaled
+        # FP8 MFMA (x and mid as two E4M3 terms), against the widening rows;
+        # their CPU baseline is the FP8 rows' (same weights and semantics)
         for wfmt, tag in ((M.WFMT_FP8_E4M3, "fp8_e4m3"), (M.WFMT_FP8_E5M2, "fp8_e5m2"),
+                          (M.WFMT_FP8_E4M3_F8X2, "fp8_e4m3_f8x2"), (M.WFMT_FP8_E5M2_F8X2, "fp8_e5m2_f8x2"),
                           (M.WFMT_INT8, "int8"), (M.WFMT_INT4, "int4_g32"), (M.WFMT_W8A8, "w8a8")):
             if not want("c3", tag):
                 continue
             fb = 4 if wfmt == M.WFMT_INT4 else 1  # fmt_bytes' format code (INT4 or 8-bit)
             wb = 3 * fmt_bytes(fb, 14336, 4096)
             r, _ = run_config(dev, M, f"C3 {tag}", None, 128, 4096, 14336, sets_for(fmt_bytes(fb, 4096, 14336)),
-                              40, 4, seed=7, wfmt=wfmt, cpu=cpu and 128)
+                              40, 4, seed=7, wfmt=wfmt, cpu=cpu and not tag.endswith("_f8x2") and 128)
             r["hbm_frac"] = round(wb / (r["us_per_iter"] * 1e-6) / HBM_PEAK, 4)
             # the longest format GEMM against HBM (weights + activations per launch)
             r["roofline"] = secondary_roofline(r, 128, 4096, 14336, None, wfmt=fb)

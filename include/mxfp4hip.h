@@ -86,7 +86,15 @@ enum {
   MX_WFMT_FP8_E5M2 = 2, /* [N][K] E5M2 + f32 row scale [N] (amax/57344) */
   MX_WFMT_INT8 = 3,     /* [N][K] int8 + f32 row scale [N] (amax/127)   */
   MX_WFMT_INT4 = 4,     /* [N][K/2] int4 (low nibble = even k) + f16 scale [N][K/32] (amax/7) */
-  MX_WFMT_W8A8 = 5      /* int8 weights as MX_WFMT_INT8, int8 activations per token, i32 accumulate */
+  MX_WFMT_W8A8 = 5,     /* int8 weights as MX_WFMT_INT8, int8 activations per token, i32 accumulate */
+  /* The FP8 rows on the FP8 matrix cores: weights exactly as MX_WFMT_FP8_E4M3 /
+   * MX_WFMT_FP8_E5M2; x and mid are split into two FP8 E4M3 terms with an
+   * E8M0 pair per 64 K (as MX_MLP_SCALED: relative error <= 2^-8 per value)
+   * and v_mfma_scale_f32_32x32x64_f8f6f4 multiplies them by the FP8 weight
+   * codes with no widening; the f32 row scale is applied to the sums.  One
+   * more launch (the split of x).  Hidden and intermediate % 64. */
+  MX_WFMT_FP8_E4M3_F8X2 = 6,
+  MX_WFMT_FP8_E5M2_F8X2 = 7
 };
 
 /* MLPConfig (main.swift:62-66, MPPMLPKernels.metal:8-12). */
@@ -280,12 +288,13 @@ int mx_load_mxfp4(mx_ctx* ctx, const char* path, const char* blocks_name, const 
                   mx_qmatrix* out, int* count_out, int* n_out, int* k_out);
 
 /* ---- weight-format rows (config 3) ------------------------------------------ */
-/* Quantize f32 weights [rows][k] into format `wfmt` (scales per the enum). */
+/* Quantize f32 weights [rows][k] into format `wfmt` (scales per the enum;
+ * the _F8X2 codes quantize as their FP8 format). */
 int mx_fmt_quantize(mx_ctx* ctx, int wfmt, const float* w, int rows, int k, void* q,
                     void* scales);
 /* MLP with format weights: mpp_mlp_h_fp8e4m3_f_n128 / _h_fp8e5m2_f_n128 /
  * h_i8_f / h_i4_f / i8_i8_i32 rows (MPPMLPKernels.metal:50-125) with scales.
- * hidden and intermediate % 32; W8A8 % 128. */
+ * hidden and intermediate % 32; the _F8X2 rows % 64; W8A8 % 128. */
 int mx_fmt_mlp_forward(mx_ctx* ctx, int wfmt, const mx_mlp_config* cfg, const void* x,
                        const mx_mlp_weights* w, void* out);
 /* Timed loop of the format rows, as mx_mlp_benchmark (kernel_us_out and

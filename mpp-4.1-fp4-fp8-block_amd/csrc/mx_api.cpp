@@ -1005,6 +1005,8 @@ int mx_fmt_quantize(mx_ctx* c, int wfmt, const float* w, int rows, int k, void* 
   if (rows <= 0 || k <= 0 || k % 32) return set_err(c, MX_EINVAL, "format quantize needs k % 32 == 0.");
   if (!w || !q || !scales || !aligned16(w) || !aligned16(q))
     return set_err(c, MX_EINVAL, "format quantize buffers must be non-null and 16-byte aligned.");
+  if (wfmt == MX_WFMT_FP8_E4M3_F8X2 || wfmt == MX_WFMT_FP8_E5M2_F8X2)
+    wfmt = wfmt == MX_WFMT_FP8_E4M3_F8X2 ? MX_WFMT_FP8_E4M3 : MX_WFMT_FP8_E5M2;  // same weights
   switch (wfmt) {
     case MX_WFMT_FP8_E4M3:
     case MX_WFMT_FP8_E5M2:
@@ -1032,6 +1034,8 @@ static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const 
     case MX_WFMT_INT8: bk = mx::BK_INT8; break;
     case MX_WFMT_INT4: bk = mx::BK_INT4G32; break;
     case MX_WFMT_W8A8: bk = mx::BK_I8; break;
+    case MX_WFMT_FP8_E4M3_F8X2: bk = mx::BK_E4M3; break;
+    case MX_WFMT_FP8_E5M2_F8X2: bk = mx::BK_E5M2; break;
     default: return set_err(c, MX_EINVAL, "Unknown weight format %d.", wfmt);
   }
   const mx_qmatrix* mats[3] = {&w->gate, &w->up, &w->down};
@@ -1065,6 +1069,38 @@ static int build_fmt_steps(mx_ctx* c, int wfmt, const mx_mlp_config* cfg, const 
     steps.push_back({"gemm_q_w8a8_gate_up_swiglu", [=] { return mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_SWIGLU_F32, gu, st); }});
     steps.push_back({"quant_mid_int8", [=] { return mx::launch_quant_act_int8(mid, MX_DTYPE_F32, T, I, mq, ms, st); }});
     steps.push_back({"gemm_q_w8a8_down", [=] { return mx::launch_gemm_q(mx::AK_I8, mx::BK_I8, mx::EPI_STORE_F16, dn, st); }});
+    return MX_OK;
+  }
+  if (wfmt == MX_WFMT_FP8_E4M3_F8X2 || wfmt == MX_WFMT_FP8_E5M2_F8X2) {
+    // FP8 weights on the FP8 matrix cores: x and mid as F8X2 (two E4M3
+    // terms + E8M0 pairs per 64 K), the weight codes as the scaled MFMA's
+    // second operand at scale 1.0, the row scales applied to the sums.
+    if (H % 64 || I % 64)
+      return set_err(c, MX_EINVAL, "The F8X2 format rows need hidden and intermediate to be multiples of 64.");
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
+    const size_t o_xq = take(mx::f8x2_data_bytes(T, H)), o_xe = take(mx::f8x2_e8_bytes(T, H)),
+                 o_mq = take(mx::f8x2_data_bytes(T, I)), o_me = take(mx::f8x2_e8_bytes(T, I)),
+                 o_qws = take(std::max(mx::gemm_q_ws_bytes(mx::AK_F8X2, bk, mx::EPI_SWIGLU_F8X2, T, I, H),
+                                       mx::gemm_q_ws_bytes(mx::AK_F8X2, bk, mx::EPI_STORE_F16, T, H, I)));
+    if (int rc = ensure_ws(c, off)) return rc;
+    uint8_t* ws = static_cast<uint8_t*>(c->ws);
+    uint8_t* xq = ws + o_xq;
+    uint32_t* xe = reinterpret_cast<uint32_t*>(ws + o_xe);
+    uint8_t* mq = ws + o_mq;
+    uint32_t* me = reinterpret_cast<uint32_t*>(ws + o_me);
+    void* qws = ws + o_qws;
+    mx::QGemmArgs gu{xq, nullptr, w->gate.data, w->gate.scales, w->up.data, w->up.scales, mq, qws, T, I, H, 0,
+                     xe, me, static_cast<const uint16_t*>(x)};
+    mx::QGemmArgs dn{mq, nullptr, w->down.data, w->down.scales, nullptr, nullptr, out, qws, T, H, I, 0, me,
+                     nullptr};
+    steps.push_back({"split_x_f8x2", [=] {
+                       return mx::launch_split_f8x2(static_cast<const uint16_t*>(x), T, H, xq, xe, st);
+                     }});
+    steps.push_back({"gemm_q_f8x2_fmt_gate_up_swiglu",
+                     [=] { return mx::launch_gemm_q(mx::AK_F8X2, bk, mx::EPI_SWIGLU_F8X2, gu, st); }});
+    steps.push_back({"gemm_q_f8x2_fmt_down",
+                     [=] { return mx::launch_gemm_q(mx::AK_F8X2, bk, mx::EPI_STORE_F16, dn, st); }});
     return MX_OK;
   }
   const size_t mid_b = align_up((size_t)T * I * 2, 256);
@@ -1106,8 +1142,10 @@ const char* mx_fmt_mlp_kernel_name(int wfmt, const mx_mlp_config* cfg, int index
   static const char* w8a8[] = {"quant_x_int8", "gemm_q_w8a8_gate_up_swiglu", "quant_mid_int8", "gemm_q_w8a8_down"};
   static const char* q[] = {"gemm_q_fmt_gate_up_swiglu", "gemm_q_fmt_down"};
   static const char* h[] = {"gemm_h_fmt_gate_up_swiglu", "gemm_h_fmt_down"};
-  if (index < 0 || !cfg || wfmt < MX_WFMT_FP8_E4M3 || wfmt > MX_WFMT_W8A8) return nullptr;
+  static const char* f8x2[] = {"split_x_f8x2", "gemm_q_f8x2_fmt_gate_up_swiglu", "gemm_q_f8x2_fmt_down"};
+  if (index < 0 || !cfg || wfmt < MX_WFMT_FP8_E4M3 || wfmt > MX_WFMT_FP8_E5M2_F8X2) return nullptr;
   if (wfmt == MX_WFMT_W8A8) return index < 4 ? w8a8[index] : nullptr;
+  if (wfmt == MX_WFMT_FP8_E4M3_F8X2 || wfmt == MX_WFMT_FP8_E5M2_F8X2) return index < 3 ? f8x2[index] : nullptr;
   if (index >= 2) return nullptr;
   const int bk = wfmt == MX_WFMT_FP8_E4M3 ? mx::BK_E4M3 : wfmt == MX_WFMT_FP8_E5M2 ? mx::BK_E5M2
                  : wfmt == MX_WFMT_INT8 ? mx::BK_INT8 : mx::BK_INT4G32;

@@ -176,6 +176,33 @@ __device__ inline float ref_dot_f8x2_mxfp4(const uint8_t* data, const uint32_t* 
   return acc;
 }
 
+// One FP8 weight byte -> f32: E4M3 (0x7f / 0xff NaN, no infinities) or E5M2
+// (IEEE-like: infinities and NaNs).
+template <bool E5M2>
+__device__ __forceinline__ float fp8_to_f32(uint32_t byte) {
+  if constexpr (E5M2) return __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(byte & 255u, 1.0f, false)[0];
+  else return e4m3_to_f32(byte);
+}
+
+// sum_k x[k] * W[k] for one f16 activation row and one FP8 weight row
+// (codes only: the caller applies the row scale).
+template <bool E5M2>
+__device__ inline float ref_dot_f16_fp8(const uint16_t* x, const uint8_t* w, int K) {
+  float acc = 0.0f;
+  for (int k = 0; k < K; k++) acc += f16_bits_to_f32(x[k]) * fp8_to_f32<E5M2>(w[k]);
+  return acc;
+}
+
+// sum_k a[row][k] * W[k] for an F8X2 activation row and one FP8 weight row
+// (codes only).
+template <bool E5M2>
+__device__ inline float ref_dot_f8x2_fp8(const uint8_t* data, const uint32_t* e8, int M, int row,
+                                         const uint8_t* w, int K) {
+  float acc = 0.0f;
+  for (int k = 0; k < K; k++) acc += f8x2_ref_value(data, e8, M, K, row, k) * fp8_to_f32<E5M2>(w[k]);
+  return acc;
+}
+
 // E8M0 byte of (row, 32-K block b) in a stage-major scale plane: [K/128]
 // planes of `rows` dwords, each the four bytes of one row's 128-K stage.
 __device__ __forceinline__ uint32_t e8m0_stage_major(const uint8_t* s, size_t rows, int row, int b) {

@@ -173,6 +173,35 @@ __device__ __forceinline__ float scaled(float acc, const QGemmArgs& g, const flo
   return v;
 }
 
+// Reference-semantics raw dot products (row scales applied by the caller)
+// for the exact recomputation of non-finite outputs of the F8X2 path: f16
+// activation row x weight row `ch` (gate / up), and F8X2 activation row x
+// weight row `col` (down).  MXFP4 weights are dequantized as the reference
+// does (E8M0 byte 255 -> +inf), FP8 codes decoded as they are.
+template <int BK>
+__device__ inline float ref_dot_f16_w(const uint16_t* xr, const void* w, const void* s, int ch, int K) {
+  const uint8_t* wb = reinterpret_cast<const uint8_t*>(w);
+  if constexpr (BK == BK_MXFP4)
+    return ref_dot_f16_mxfp4(xr, wb + (size_t)ch * (K / 2), reinterpret_cast<const uint8_t*>(s) + (size_t)ch * (K / 32), K);
+  else
+    return ref_dot_f16_fp8<BK == BK_E5M2>(xr, wb + (size_t)ch * K, K);
+}
+template <int BK>
+__device__ inline float ref_dot_f8x2_w(const uint8_t* ad, const uint32_t* ae, int M, int row, const void* w,
+                                       const void* s, int col, int K) {
+  const uint8_t* wb = reinterpret_cast<const uint8_t*>(w);
+  if constexpr (BK == BK_MXFP4)
+    return ref_dot_f8x2_mxfp4(ad, ae, M, row, wb + (size_t)col * (K / 2),
+                              reinterpret_cast<const uint8_t*>(s) + (size_t)col * (K / 32), K);
+  else
+    return ref_dot_f8x2_fp8<BK == BK_E5M2>(ad, ae, M, row, wb + (size_t)col * K, K);
+}
+// Row scale of weight row `col` (1 for formats without one).
+template <int BK>
+__device__ __forceinline__ float row_scale(const void* s, int col) {
+  return row_scaled(BK) ? reinterpret_cast<const float*>(s)[col] : 1.0f;
+}
+
 constexpr int out_bytes(int epi) {
   return epi == EPI_STORE_F32 || epi == EPI_STORE_I32 || epi == EPI_SWIGLU_F32 ? 4 : 2;
 }
@@ -274,7 +303,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   const int KT = K / KS / (int)gridDim.y;     // stages of this split
   const int kt0 = (int)blockIdx.y * KT;
   const size_t a_row = (size_t)K * (AK == AK_F32 ? 4 : (AK == AK_F16 || AK == AK_F8X2) ? 2 : 1);
-  static_assert(AK != AK_F8X2 || (BK == BK_MXFP4 && !GROUPED), "F8X2 activations: MXFP4 weights on the scaled MFMA");
+  static_assert(AK != AK_F8X2 || ((BK == BK_MXFP4 || BK == BK_E4M3 || BK == BK_E5M2) && !GROUPED),
+                "F8X2 activations: MXFP4 or FP8 weights on the scaled MFMA");
   const size_t b_row = (size_t)b_row_bytes<BK>(K);
 
   // ---- DMA sources (per lane, per instruction)
@@ -465,7 +495,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     _Pragma("unroll") for (int u = 0; u < BREADS; u++) {                                           \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                            \
         const int r_ = b_blk[j] + r32;                                                             \
-        const int ch_ = (CO) + (BREADS == 1 ? h : BREADS == 2 ? 2 * h + u : 4 * h + u);            \
+        /* FP8 weights under F8X2 activations: the scaled MFMA's 8-bit operand */                \
+        /* layout, k [16h, +16) then [32 + 16h, +16), i.e. chunks h and h + 2 */                  \
+        const int ch_ = (CO) + (BREADS == 1 ? h : BREADS == 2 ? (AK == AK_F8X2 ? h + 2 * u : 2 * h + u) : 4 * h + u); \
         BR[u][j] = *reinterpret_cast<const v4i*>((BS) + r_ * RBC + ((ch_ ^ swz<RBC>(r_)) << 4));  \
       }                                                                                            \
     }                                                                                              \
@@ -480,7 +512,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // v_mfma_scale_f32_32x32x64_f8f6f4 (A E4M3 term t with its E8M0 byte t
   // of the pair, B FP4 with the lane's E8M0 byte) into one accumulator.
   // Lane half h of both operands holds 32-block h of the stage, so the
-  // lane's own scale bytes are the ones each operand needs.
+  // lane's own scale bytes are the ones each operand needs.  FP8 weights
+  // (E4M3 / E5M2 codes, f32 row scale applied in the epilogue) go in as the
+  // B operand at E8M0 127 (1.0): 32 bytes per lane, k [16h, +16) and
+  // [32 + 16h, +16) of the stage, the same 8-bit layout as the A terms.
 #define MXQ_MATH_F8X2(AR, BR, P)                                                                   \
   {                                                                                                \
     _Pragma("unroll") for (int i = 0; i < 2; i++) {                                                \
@@ -491,11 +526,18 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       }                                                                                            \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                            \
         v8i b_;                                                                                    \
-        _Pragma("unroll") for (int t = 0; t < 4; t++) { b_[t] = BR[0][j][t]; b_[4 + t] = 0; }      \
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a1_, b_, (v16f)acc[i][j], 0, 4, 0, \
-                                                                    (int)AR##_sc[i], 0, (int)scv[P][j]); \
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a2_, b_, (v16f)acc[i][j], 0, 4, 1, \
-                                                                    (int)AR##_sc[i], 0, (int)scv[P][j]); \
+        if constexpr (BK == BK_MXFP4) {                                                            \
+          _Pragma("unroll") for (int t = 0; t < 4; t++) { b_[t] = BR[0][j][t]; b_[4 + t] = 0; }    \
+        } else {                                                                                   \
+          _Pragma("unroll") for (int t = 0; t < 4; t++) { b_[t] = BR[0][j][t]; b_[4 + t] = BR[1][j][t]; } \
+        }                                                                                          \
+        /* B format: FP4 (4) with the row's E8M0 byte, or E4M3 (0) / E5M2 (1) at scale 1.0 */      \
+        constexpr int BF_ = BK == BK_MXFP4 ? 4 : BK == BK_E4M3 ? 0 : 1;                            \
+        const int bs_ = BK == BK_MXFP4 ? (int)scv[P][j] : 127;                                     \
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a1_, b_, (v16f)acc[i][j], 0, BF_, 0, \
+                                                                    (int)AR##_sc[i], 0, bs_);      \
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a2_, b_, (v16f)acc[i][j], 0, BF_, 1, \
+                                                                    (int)AR##_sc[i], 0, bs_);      \
       }                                                                                            \
     }                                                                                              \
   }
@@ -766,12 +808,15 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     uint8_t* const ms1 = NS == 2 ? a_s1 : d_s1;
     __syncthreads();
     float* ml = reinterpret_cast<float*>(wm ? ms1 : ms0);
+    // FP8 weights: the gate / up row scales of the lane's channel
+    const float csg = row_scale<BK>(g.s0, n0 + wn * 32 + r32), csu = row_scale<BK>(g.s1, n0 + wn * 32 + r32);
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int rl = i * 32 + acc32_row(lane, v), c = wn * 32 + r32;
-        const float x0 = acc[i][0][v], u = acc[i][NWB - 1][v];
+        float x0 = acc[i][0][v], u = acc[i][NWB - 1][v];
+        if (row_scaled(BK)) { x0 = x0 * csg; u = u * csu; }
         ml[rl * 64 + (c ^ (rl & 31))] = (x0 / (1.0f + expf(-x0))) * u;
       }
     __syncthreads();
@@ -794,17 +839,13 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     if (__builtin_expect(__ballot(nf != 0) != 0, 0)) {
       if (nf && row < M && g.a_f16) {
         const uint16_t* xr = g.a_f16 + (size_t)row * K;
-        const uint8_t* wg = reinterpret_cast<const uint8_t*>(g.b0);
-        const uint8_t* wu = reinterpret_cast<const uint8_t*>(g.b1);
-        const uint8_t* sg = reinterpret_cast<const uint8_t*>(g.s0);
-        const uint8_t* su = reinterpret_cast<const uint8_t*>(g.s1);
 #pragma nounroll
         for (int k = 0; k < 32; k++) {
           const int c = 32 * half + k, ch = n0 + c;
           float* p = src + rl * 64 + (c ^ (rl & 31));
           if ((__builtin_bit_cast(uint32_t, *p) & 0x7fffffffu) >= 0x7f800000u) {
-            const float gv = ref_dot_f16_mxfp4(xr, wg + (size_t)ch * (K / 2), sg + (size_t)ch * (K / 32), K);
-            const float uv = ref_dot_f16_mxfp4(xr, wu + (size_t)ch * (K / 2), su + (size_t)ch * (K / 32), K);
+            float gv = ref_dot_f16_w<BK>(xr, g.b0, g.s0, ch, K), uv = ref_dot_f16_w<BK>(xr, g.b1, g.s1, ch, K);
+            if (row_scaled(BK)) { gv = gv * row_scale<BK>(g.s0, ch); uv = uv * row_scale<BK>(g.s1, ch); }
             *p = (gv / (1.0f + expf(-gv))) * uv;
           }
         }
@@ -886,8 +927,6 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
         }
     if (__builtin_expect(__ballot(nanm != 0) != 0, 0)) {
       const uint8_t* ad = reinterpret_cast<const uint8_t*>(g.a);
-      const uint8_t* wb = reinterpret_cast<const uint8_t*>(g.b0);
-      const uint8_t* sb = reinterpret_cast<const uint8_t*>(g.s0);
 #pragma nounroll
       for (int e = 0; e < 2 * NWB * 16; e++) {
         if (!((nanm >> e) & 1u)) continue;
@@ -895,7 +934,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
         const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, v);
         const int col = n0 + b_blk[jj] + r32;
         if (row >= M) continue;
-        const float r = ref_dot_f8x2_mxfp4(ad, g.a_e8, M, row, wb + (size_t)col * (K / 2), sb + (size_t)col * (K / 32), K);
+        float r = ref_dot_f8x2_w<BK>(ad, g.a_e8, M, row, g.b0, g.s0, col, K);
+        if (row_scaled(BK)) r = r * row_scale<BK>(g.s0, col);
         epi_store<EPI>(g.c, (size_t)row * g.n + col, r, 0.0f);
       }
     }
@@ -930,7 +970,12 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
     }
     float mv[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) mv[c] = (gs[c] / (1.0f + expf(-gs[c]))) * us[c];
+    for (int c = 0; c < 4; c++) {
+      const int ch = grp * 64 + 4 * j + c;
+      const float gg = row_scaled(BK) ? gs[c] * row_scale<BK>(g.s0, ch) : gs[c];
+      const float uu = row_scaled(BK) ? us[c] * row_scale<BK>(g.s1, ch) : us[c];
+      mv[c] = (gg / (1.0f + expf(-gg))) * uu;
+    }
     // non-finite mid (E8M0 byte 255 in a gate / up scale, or a non-finite x):
     // recomputed from the f16 activations with the reference's dequantization
     if (g.a_f16) {
@@ -940,10 +985,8 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
         if ((__builtin_bit_cast(uint32_t, mv[c]) & 0x7fffffffu) >= 0x7f800000u) {
           const int ch = grp * 64 + 4 * j + c;
           const uint16_t* xr = g.a_f16 + (size_t)row * K;
-          const float gv = ref_dot_f16_mxfp4(xr, reinterpret_cast<const uint8_t*>(g.b0) + (size_t)ch * (K / 2),
-                                             reinterpret_cast<const uint8_t*>(g.s0) + (size_t)ch * (K / 32), K);
-          const float uv = ref_dot_f16_mxfp4(xr, reinterpret_cast<const uint8_t*>(g.b1) + (size_t)ch * (K / 2),
-                                             reinterpret_cast<const uint8_t*>(g.s1) + (size_t)ch * (K / 32), K);
+          float gv = ref_dot_f16_w<BK>(xr, g.b0, g.s0, ch, K), uv = ref_dot_f16_w<BK>(xr, g.b1, g.s1, ch, K);
+          if (row_scaled(BK)) { gv = gv * row_scale<BK>(g.s0, ch); uv = uv * row_scale<BK>(g.s1, ch); }
           mv[c] = (gv / (1.0f + expf(-gv))) * uv;
         }
       }
@@ -997,9 +1040,8 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
       // E8M0 byte 255 in a weight scale (NaN in the scaled MFMA, +inf in the
       // reference) or a non-finite activation group: recomputed with the
       // reference's dequantization
-      x0 = ref_dot_f8x2_mxfp4(reinterpret_cast<const uint8_t*>(g.a), g.a_e8, g.m, row,
-                              reinterpret_cast<const uint8_t*>(g.b0) + (size_t)(col + t) * (g.k / 2),
-                              reinterpret_cast<const uint8_t*>(g.s0) + (size_t)(col + t) * (g.k / 32), g.k);
+      x0 = ref_dot_f8x2_w<BK>(reinterpret_cast<const uint8_t*>(g.a), g.a_e8, g.m, row, g.b0, g.s0, col + t, g.k);
+      if (row_scaled(BK)) x0 = x0 * row_scale<BK>(g.s0, col + t);
     }
     epi_store<EPI>(g.c, o + t, x0, u);
   }
@@ -1187,7 +1229,9 @@ bool gemm_q_ok(int ak, int bk, int epi, int m, int n, int k) {
   if (n % 64) return false;
   if (ak == AK_I8)
     return bk == BK_I8 && (epi == EPI_SWIGLU_F32 || epi == EPI_STORE_F16 || epi == EPI_STORE_F32 || epi == EPI_STORE_I32);
-  if (ak == AK_F8X2) return bk == BK_MXFP4 && (epi == EPI_SWIGLU_F8X2 || epi == EPI_STORE_F16 || epi == EPI_STORE_F32);
+  if (ak == AK_F8X2)
+    return (bk == BK_MXFP4 || bk == BK_E4M3 || bk == BK_E5M2) &&
+           (epi == EPI_SWIGLU_F8X2 || epi == EPI_STORE_F16 || epi == EPI_STORE_F32);
   return bk != BK_I8 && epi != EPI_STORE_I32 && epi != EPI_SWIGLU_F32 && epi != EPI_SWIGLU_F8X2;
 }
 
@@ -1225,13 +1269,18 @@ hipError_t launch_gemm_q(int ak, int bk, int epi, const QGemmArgs& g, hipStream_
       default: return hipErrorInvalidValue;
     }
   }
-  if (ak == AK_F8X2) {  // MXFP4 weights only (gemm_q_ok)
-    switch (epi) {
-      case EPI_SWIGLU_F8X2: return launch_wn<AK_F8X2, BK_MXFP4, EPI_SWIGLU_F8X2>(g, s, st);
-      case EPI_STORE_F16: return launch_wn<AK_F8X2, BK_MXFP4, EPI_STORE_F16>(g, s, st);
-      case EPI_STORE_F32: return launch_wn<AK_F8X2, BK_MXFP4, EPI_STORE_F32>(g, s, st);
-      default: return hipErrorInvalidValue;
+  if (ak == AK_F8X2) {  // MXFP4 or FP8 weights (gemm_q_ok)
+#define MXQ_F8X2(BK)                                                                                \
+    switch (epi) {                                                                                  \
+      case EPI_SWIGLU_F8X2: return launch_wn<AK_F8X2, BK, EPI_SWIGLU_F8X2>(g, s, st);              \
+      case EPI_STORE_F16: return launch_wn<AK_F8X2, BK, EPI_STORE_F16>(g, s, st);                  \
+      case EPI_STORE_F32: return launch_wn<AK_F8X2, BK, EPI_STORE_F32>(g, s, st);                  \
+      default: return hipErrorInvalidValue;                                                         \
     }
+    if (bk == BK_MXFP4) { MXQ_F8X2(BK_MXFP4) }
+    if (bk == BK_E4M3) { MXQ_F8X2(BK_E4M3) }
+    MXQ_F8X2(BK_E5M2)
+#undef MXQ_F8X2
   }
   if (ak == AK_F32) {
     if (epi != EPI_STORE_F32 && epi != EPI_STORE_F16) return hipErrorInvalidValue;

@@ -20,6 +20,7 @@ FMT_FP4_E2M1, FMT_FP8_E4M3, FMT_FP8_E5M2 = range(3)
 MLP_FUSED, MLP_DEQUANT, MLP_W4A4, MLP_REFROW, MLP_SCALED = range(5)
 PROBE_F16, PROBE_FP4, PROBE_FP8, PROBE_INT4, PROBE_I8 = range(5)
 WFMT_FP8_E4M3, WFMT_FP8_E5M2, WFMT_INT8, WFMT_INT4, WFMT_W8A8 = 1, 2, 3, 4, 5
+WFMT_FP8_E4M3_F8X2, WFMT_FP8_E5M2_F8X2 = 6, 7  # FP8 weights on the scaled FP8 MFMA (F8X2 activations)
 
 # Every symbol the header declares (checked by tests/test_abi_exports.py).
 EXPORTS = [

@@ -125,3 +125,78 @@ def test_int4_scale_planes_4_byte_aligned(dev):
     for b in shifted:
         b.free()
     d.free()
+
+
+# ---- FP8 rows on the FP8 matrix cores (MX_WFMT_FP8_*_F8X2) -------------------
+# Same weights and reference semantics as MX_WFMT_FP8_E4M3 / _E5M2 (the
+# oracle's modes 1 / 2); x and mid go in as two E4M3 terms per value (F8X2,
+# relative error <= 2^-8 each), so the rows are held to the BASELINE
+# tolerance against the oracle and to 1e-2 of rms against the widening row.
+F8X2_FMTS = [(M.WFMT_FP8_E4M3_F8X2, M.WFMT_FP8_E4M3), (M.WFMT_FP8_E5M2_F8X2, M.WFMT_FP8_E5M2)]
+
+
+# T: ragged single tiles (1, 17), a full tile's worth (64), two tiles with a
+# partial one (130); H = 512 / I = 1024 split K in both GEMMs
+@pytest.mark.parametrize("fmt,base", F8X2_FMTS)
+@pytest.mark.parametrize("T", [1, 17, 64, 130])
+def test_f8x2_format_mlp_small(dev, fmt, base, T):
+    d = MlpData(dev, T, 512, 1024, seed=300 + T + fmt, wfmt=base)
+    got = run_fmt(dev, d, fmt)
+    rel, cos = O.mlp_error(got, oracle_fmt(d, base))
+    print(f"fmt {fmt} T={T}: rel={rel:.3e} cos={cos:.7f}", flush=True)
+    assert np.isfinite(got.astype(np.float64)).all()
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    # deterministic (split-K partials summed in a fixed order)
+    assert np.array_equal(run_fmt(dev, d, fmt).view(np.uint16), got.view(np.uint16))
+    rel2, cos2 = O.mlp_error(got, run_fmt(dev, d, base).astype(np.float64))
+    assert rel2 <= 1e-2 and cos2 >= 0.99999, (rel2, cos2)
+    d.free()
+
+
+@pytest.mark.parametrize("fmt,base", F8X2_FMTS)
+def test_f8x2_config3(dev, fmt, base):
+    """C3 shape: gate/up on the deep ring unsplit (224 tiles), down on the
+    deep ring with 8 K splits and the reduce."""
+    d = MlpData(dev, 128, 4096, 14336, seed=41 + fmt, wfmt=base)
+    rows = sample_rows(128, 16)
+    got = run_fmt(dev, d, fmt)[rows]
+    rel, cos = O.mlp_error(got, oracle_fmt(d, base, rows=rows))
+    print(f"C3 fmt {fmt}: rel={rel:.3e} cos={cos:.7f}", flush=True)
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    d.free()
+
+
+@pytest.mark.parametrize("fmt,base", F8X2_FMTS)
+@pytest.mark.parametrize("T,H,I", [(64, 512, 256), (128, 1024, 4096)])
+def test_f8x2_nonfinite_x(dev, fmt, base, T, H, I):
+    """A non-finite activation cannot be an F8X2 term: its group is marked
+    (E8M0 255, NaN in the MFMA) and the outputs it reaches are recomputed
+    with the reference's arithmetic, so NaN, +inf and -inf land where the
+    oracle's do.  Token 0 holds +inf, token 1 -inf, token 2 NaN; (64, 512,
+    256) stores from the GEMM epilogues, (128, 1024, 4096) from the split-K
+    reduces."""
+    d = MlpData(dev, T, H, I, seed=61 + fmt, wfmt=base)
+    x = dev.download(d.x, np.float16, (T, H))
+    x[0, 5] = np.inf
+    x[1, 70] = -np.inf
+    x[2, 300] = np.nan
+    dev.upload(x, d.x)
+    got = run_fmt(dev, d, fmt).astype(np.float64)
+    ref = oracle_fmt(d, base).astype(np.float64)
+    assert not np.isfinite(ref[:3]).any()
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), (np.isnan(got).sum(), np.isnan(ref).sum())
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    rel, cos = O.mlp_error(got[3:], ref[3:])
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL, (rel, cos)
+    d.free()
+
+
+def test_f8x2_format_rejects_bad_shapes(dev):
+    d = MlpData(dev, 4, 256, 512, seed=3, wfmt=M.WFMT_FP8_E4M3)
+    out = dev.alloc(4 * 256 * 2)
+    with pytest.raises(M.MxError) as e:
+        dev.fmt_mlp_forward(M.WFMT_FP8_E4M3_F8X2, 4, 96, 512, d.x, d.weights, out)  # hidden % 64
+    assert e.value.code == M.MX_EINVAL
+    out.free()
+    d.free()
