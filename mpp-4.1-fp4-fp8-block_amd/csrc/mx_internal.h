@@ -108,6 +108,12 @@ bool gemm_q_ok(int akind, int bkind, int epi, int m, int n, int k);
 size_t gemm_q_ws_bytes(int akind, int bkind, int epi, int m, int n, int k);
 int gemm_q_splits(int akind, int bkind, int epi, int m, int n, int k);
 hipError_t launch_gemm_q(int akind, int bkind, int epi, const QGemmArgs& g, hipStream_t st);
+// Few-tile MXFP4 GEMMs (mx_gemm_small.hip): f16 activations, at most 128
+// rows; the dual gate/up + SwiGLU at K = 1024, or a plain GEMM with
+// K % 1024 == 0 (<= 4096) and N % 32 == 0 (<= 2048).  launch_gemm_q takes
+// this path for AK_F16 x BK_MXFP4 shapes it accepts.
+bool small_gemm_ok(int epi, int m, int n, int k);
+hipError_t launch_small_gemm(int epi, const QGemmArgs& g, hipStream_t st);
 // Grouped (MoE) form, MXFP4 weights and f16 activations only; g.m = the
 // largest group's rows, epi EPI_SWIGLU_F16 or EPI_STORE_F16, no split K.
 hipError_t launch_gemm_q_grouped(int epi, const QGemmArgs& g, const GroupTable& gt, int groups, hipStream_t st);
