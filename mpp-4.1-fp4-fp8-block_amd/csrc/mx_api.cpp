@@ -284,6 +284,9 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
     const int e_dn = ref ? mx::EPI_STORE_F32 : mx::EPI_STORE_F16;
     void* qws = ws + s.qws;
     mx::QGemmArgs gu{x, nullptr, wg, sg, wu, su, mid, qws, T, I, H, 0};
+    gu.pf = wd;  // the down weights, pulled into L2 by the few-tile gate/up kernel
+    gu.pf_rows = H;
+    gu.pf_row_bytes = I / 2;
     mx::QGemmArgs dn{mid, nullptr, wd, sd, nullptr, nullptr, out, qws, T, H, I, 0};
     steps.push_back({ref ? "gemm_q_mxfp4_gate_up_swiglu_half" : "gemm_q_mxfp4_gate_up_swiglu",
                      [=] { return mx::launch_gemm_q(mx::AK_F16, mx::BK_MXFP4, e_gu, gu, st); }});

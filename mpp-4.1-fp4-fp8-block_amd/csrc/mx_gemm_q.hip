@@ -1259,7 +1259,10 @@ hipError_t launch_gemm_q_grouped(int epi, const QGemmArgs& g, const GroupTable& 
 hipError_t launch_gemm_q(int ak, int bk, int epi, const QGemmArgs& g, hipStream_t st) {
   if (!gemm_q_ok(ak, bk, epi, g.m, g.n, g.k)) return hipErrorInvalidValue;
   // few tiles (C0): one small tile per CU, operands requested up front
-  if (ak == AK_F16 && bk == BK_MXFP4 && small_gemm_ok(epi, g.m, g.n, g.k)) return launch_small_gemm(epi, g, st);
+  // (its scale loads are dwords: planes at a 4-byte boundary)
+  if (ak == AK_F16 && bk == BK_MXFP4 && small_gemm_ok(epi, g.m, g.n, g.k) &&
+      ((reinterpret_cast<uintptr_t>(g.s0) | reinterpret_cast<uintptr_t>(g.s1)) & 3u) == 0)
+    return launch_small_gemm(epi, g, st);
   const int s = gemm_q_splits(ak, bk, epi, g.m, g.n, g.k);
   if (s > 1 && !g.ws) return hipErrorInvalidValue;
   if (ak == AK_I8) {

@@ -73,6 +73,7 @@ __global__ __launch_bounds__(512) void k_small_gate_up(QGemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t a_s2[4 * 32 * 128];
   __shared__ __attribute__((aligned(16))) uint8_t a_s3[4 * 32 * 128];
   __shared__ __attribute__((aligned(16))) uint8_t b_lds[8 * 64 * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t pf_lds[512 * 16];  // prefetch landing, never read
 #define MXS_A(ST) ((ST) == 0 ? a_s0 : (ST) == 1 ? a_s1 : (ST) == 2 ? a_s2 : a_s3)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -119,6 +120,30 @@ __global__ __launch_bounds__(512) void k_small_gate_up(QGemmArgs g) {
     }
   }
 
+  // 3b. One 16-byte DMA per thread pulls a share of the next GEMM's weights
+  //    (g.pf) into this XCD's L2: the rows whose 32-row tile the plain
+  //    kernel's grid places on this XCD (tile t on XCD t % 8, the workgroup
+  //    order's round robin), split over this XCD's workgroups.  Issued
+  //    behind this kernel's own loads, it overlaps their latency; the next
+  //    kernel then starts on L2 hits (C0's down GEMM: first data 2.7 ->
+  //    1.7 us).  Every thread issues it (a dummy address without g.pf), so
+  //    the stage waits below count it.
+  {
+    const uint8_t* src = x;
+    if (g.pf && g.pf_rows % 256 == 0) {
+      const int xcd = (int)(blockIdx.x & 7), nwg = ((int)gridDim.x - xcd + 7) / 8, i = (int)(blockIdx.x >> 3);
+      const int rb = g.pf_row_bytes;
+      const long pieces = (long)(g.pf_rows / 8) * (rb / 16);  // 16-byte pieces on this XCD
+      const long share = (pieces + nwg - 1) / nwg;
+      long pc = (long)i * share + tid;
+      if (pc >= pieces) pc = pieces - 1;
+      const long off = pc * 16;
+      const int rl = (int)(off / rb), n = (rl / 32) * 256 + xcd * 32 + rl % 32;
+      src = reinterpret_cast<const uint8_t*>(g.pf) + (size_t)n * rb + off % rb;
+    }
+    dma16(src, pf_lds + wave * 1024);
+  }
+
   v16f acc[2];
 #pragma unroll
   for (int b = 0; b < 2; b++)
@@ -131,7 +156,7 @@ __global__ __launch_bounds__(512) void k_small_gate_up(QGemmArgs g) {
 #define MXS_STAGE(ST)                                                                              \
   {                                                                                                \
     __builtin_amdgcn_sched_barrier(0);                                                             \
-    __builtin_amdgcn_s_waitcnt(wait_vm(2 * (3 - (ST))));                                           \
+    __builtin_amdgcn_s_waitcnt(wait_vm(2 * (3 - (ST)) + 1)); /* + the prefetch DMA */             \
     __builtin_amdgcn_s_barrier();                                                                  \
     __builtin_amdgcn_sched_barrier(0);                                                             \
     const uint8_t* as_ = MXS_A(ST) + kq * 32 * 128;                                                \
@@ -163,39 +188,49 @@ __global__ __launch_bounds__(512) void k_small_gate_up(QGemmArgs g) {
 #undef MXS_STAGE
 #undef MXS_A
 
-  // 5. K quarters 1..3 park their sums in LDS; quarter 0 adds them in order
-  //    (deterministic), applies the SwiGLU and stores mid.
+  // 5. Every wave parks its sums in LDS ([kq][cb][b][v][lane], 64 KB over
+  //    B); wave (cb, kq) then adds the four K quarters in order
+  //    (deterministic) for its accumulator rows v = 4 kq .. 4 kq + 3, applies
+  //    the SwiGLU and writes mid into an f16 tile [32 rows][64 channels] in
+  //    LDS, which goes out as one 16-byte store per thread (per-element
+  //    stores behind row guards are serialised by the compiler: 2.8 us).
   __syncthreads();
-  float* red = reinterpret_cast<float*>(b_lds);  // [kq-1][cb][b][v][lane], 48 KB
-  if (kq > 0) {
+  v4f* red = reinterpret_cast<v4f*>(b_lds);  // [kq][cb][b][v / 4][lane] x 4 floats
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+  for (int b = 0; b < 2; b++)
 #pragma unroll
-      for (int v = 0; v < 16; v++) red[((((kq - 1) * 2 + cb) * 2 + b) * 16 + v) * 64 + lane] = acc[b][v];
+    for (int vq = 0; vq < 4; vq++)
+      red[(((kq * 2 + cb) * 2 + b) * 4 + vq) * 64 + lane] =
+          (v4f){acc[b][4 * vq], acc[b][4 * vq + 1], acc[b][4 * vq + 2], acc[b][4 * vq + 3]};
+  __syncthreads();
+  v4f sum[2];
+#pragma unroll
+  for (int b = 0; b < 2; b++) {
+    sum[b] = red[(((0 * 2 + cb) * 2 + b) * 4 + kq) * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < 4; q++) sum[b] += red[(((q * 2 + cb) * 2 + b) * 4 + kq) * 64 + lane];
+  }
+  uint16_t* tile = reinterpret_cast<uint16_t*>(a_s0);  // [32][64] f16, row pitch 128 B
+#pragma unroll
+  for (int vv = 0; vv < 4; vv++) {
+    const int v = 4 * kq + vv;
+    const float t[2] = {sum[0][vv], sum[1][vv]};
+    float mv;
+    if (EPI == EPI_SWIGLU_HALF) {  // swiglu_half: silu(clamp(g/16, +-20)) * u/16
+      const float gg = fminf(fmaxf(t[0] * 0.0625f, -20.0f), 20.0f);
+      mv = silu_f(gg) * (t[1] * 0.0625f);
+    } else {
+      mv = silu_f(t[0]) * t[1];
+    }
+    tile[acc32_row(lane, v) * 64 + cb * 32 + j] = f32_to_f16_bits(mv);
   }
   __syncthreads();
-  if (kq == 0) {
-    uint16_t* mid = reinterpret_cast<uint16_t*>(g.c);
-    const int col = c0 + j;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      float t[2];
-#pragma unroll
-      for (int b = 0; b < 2; b++) {
-        float s = acc[b][v];
-#pragma unroll
-        for (int q = 0; q < 3; q++) s += red[(((q * 2 + cb) * 2 + b) * 16 + v) * 64 + lane];
-        t[b] = s;
-      }
-      const int row = m0 + acc32_row(lane, v);
-      float mv;
-      if (EPI == EPI_SWIGLU_HALF) {  // swiglu_half: silu(clamp(g/16, +-20)) * u/16
-        const float gg = fminf(fmaxf(t[0] * 0.0625f, -20.0f), 20.0f);
-        mv = silu_f(gg) * (t[1] * 0.0625f);
-      } else {
-        mv = silu_f(t[0]) * t[1];
-      }
-      if (row < M) mid[(size_t)row * g.n + col] = f32_to_f16_bits(mv);
+  if (tid < 256) {  // row tid / 8, channels 8 (tid % 8) .. + 8
+    const int r = tid >> 3, row = m0 + r;
+    if (row < M) {
+      const uint4 v = *reinterpret_cast<const uint4*>(tile + r * 64 + (tid & 7) * 8);
+      const int ct = (int)(blockIdx.x % tiles_n) * 64;
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(g.c) + (size_t)row * g.n + ct + (tid & 7) * 8) = v;
     }
   }
 }
@@ -330,30 +365,36 @@ __global__ __launch_bounds__(256) void k_small_store(QGemmArgs g) {
 #undef MXS_ISSUE
 #undef MXS_SLOT
 
-  // K quarters 1..3 park their sums; quarter 0 adds them in order and stores.
+  // Every wave parks its sums ([kq][b][v][lane]); wave w adds the four K
+  // quarters in order for accumulator row v = w of both blocks, into an
+  // output tile [16 rows][32 columns] in LDS that goes out in 16-byte
+  // stores (f16: 64 threads, f32: 128).
   __syncthreads();
-  float* red = reinterpret_cast<float*>(ring0);  // [kq-1][b][v][lane], 6 KB
-  if (kq > 0) {
+  float* red = reinterpret_cast<float*>(ring0);
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+  for (int b = 0; b < 2; b++)
 #pragma unroll
-      for (int v = 0; v < 4; v++) red[(((kq - 1) * 2 + b) * 4 + v) * 64 + lane] = acc[b][v];
+    for (int v = 0; v < 4; v++) red[((kq * 2 + b) * 4 + v) * 64 + lane] = acc[b][v];
+  __syncthreads();
+  constexpr int OB = EPI == EPI_STORE_F32 ? 4 : 2;  // output bytes
+  uint8_t* tile = ring1;                            // [16][32] outputs, row pitch 32 * OB
+#pragma unroll
+  for (int b = 0; b < 2; b++) {
+    float t = red[((0 * 2 + b) * 4 + kq) * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < 4; q++) t += red[((q * 2 + b) * 4 + kq) * 64 + lane];
+    const int r = 4 * q4 + kq, cc = 16 * b + j;  // 16x16 D: row 4 (lane / 16) + v, column lane % 16
+    if (EPI == EPI_STORE_F32) reinterpret_cast<float*>(tile)[r * 32 + cc] = t;
+    else reinterpret_cast<uint16_t*>(tile)[r * 32 + cc] = f32_to_f16_bits(t);
   }
   __syncthreads();
-  if (kq == 0) {
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-      for (int v = 0; v < 4; v++) {
-        float t = acc[b][v];
-#pragma unroll
-        for (int q = 0; q < 3; q++) t += red[((q * 2 + b) * 4 + v) * 64 + lane];
-        const int row = m0 + 4 * q4 + v, col = n0 + 16 * b + j;  // 16x16 D: rows 4 (lane/16) + v, column lane % 16
-        if (row < M) {
-          if (EPI == EPI_STORE_F32) reinterpret_cast<float*>(g.c)[(size_t)row * N + col] = t;
-          else reinterpret_cast<uint16_t*>(g.c)[(size_t)row * N + col] = f32_to_f16_bits(t);
-        }
-      }
+  constexpr int PER_ROW = 32 * OB / 16;  // 16-byte pieces per output row
+  if (tid < 16 * PER_ROW) {
+    const int r = tid / PER_ROW, pc = tid % PER_ROW, row = m0 + r;
+    if (row < M) {
+      const uint4 v = *reinterpret_cast<const uint4*>(tile + r * 32 * OB + pc * 16);
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(g.c) + ((size_t)row * N + n0) * OB + pc * 16) = v;
+    }
   }
 }
 

@@ -103,6 +103,11 @@ struct QGemmArgs {
   uint32_t* c_e8;                         // EPI_SWIGLU_F8X2: mid E8M0 pairs [N/64][M]
   const uint16_t* a_f16;                  // EPI_SWIGLU_F8X2: the f16 activations the F8X2
                                           // ones were split from (exact fix-up of NaN outputs)
+  // Few-tile gate/up kernel only: weights of the GEMM that follows
+  // (pf_rows rows of pf_row_bytes), pulled into each XCD's L2 for the
+  // workgroups that will read them there (a hint; null for none).
+  const void* pf = nullptr;
+  int pf_rows = 0, pf_row_bytes = 0;
 };
 bool gemm_q_ok(int akind, int bkind, int epi, int m, int n, int k);
 size_t gemm_q_ws_bytes(int akind, int bkind, int epi, int m, int n, int k);
