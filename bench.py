@@ -42,8 +42,8 @@ sys.path.insert(0, os.path.join(ROOT, "mpp-4.1-fp4-fp8-block_amd"))
 HBM_PEAK = 8.0e12            # B/s
 PEAK = {"fp4": 10.1e15, "fp8": 5.0e15, "f16": 2.5e15, "i8": 5.0e15}
 METRIC = "MXFP4 MLP µs/iter + effective TFLOP/s (1×MI355X), % of MFMA/HBM roofline"
-DEQUANT_NOTE = ("down GEMM rounds the f32 mid to f16 for the fp16 MFMA (the reference's f_h_f "
-                "multiplies f32 x half)")
+DEQUANT_NOTE = ("down GEMM takes the f32 mid as two f16 terms (hi + lo) on the fp16 MFMA, f32 x half "
+                "as the reference's f_h_f")
 
 
 def log(*a):

@@ -55,9 +55,9 @@ enum {
    * counterpart of the native scale-plane rows (MXFP4Kernels.metal:138-173). */
   MX_MLP_FUSED = 0,
   /* dequant: 3 x dequant-to-half, h_h_f gate/up, swiglu_float, down
-   * (encodeMXFP4DequantMLP main.swift:2426-2538).  The down GEMM rounds the
-   * f32 mid to f16 for the fp16 MFMA, where the reference's f_h_f multiplies
-   * f32 x half (about 3e-3 of rms). */
+   * (encodeMXFP4DequantMLP main.swift:2426-2538).  The down GEMM takes the
+   * f32 mid as two f16 terms (hi + lo) into the fp16 MFMA, so f32 x half
+   * holds to ~2^-22 of each value as in the reference's f_h_f. */
   MX_MLP_DEQUANT = 1,
   /* W4A4: x and mid quantized to MXFP4 along K, FP4 x FP4 scaled MFMA
    * (v_mfma_scale_f32_32x32x64_f8f6f4), fp16 out. */
@@ -173,7 +173,8 @@ int mx_mxfp4_dequant_f16(mx_ctx* ctx, const uint8_t* packed, const uint8_t* scal
 int mx_mxfp4_matmul(mx_ctx* ctx, const void* a, int a_dtype, const uint8_t* b, void* c,
                     int c_dtype, int m, int n, int k, const uint8_t* scales);
 /* C f32 = A * B^T with B f16 [n][k]: mpp_mlp_h_h_f_n128 (a f16) and
- * mpp_mlp_f_h_f_n128 (a f32) (MPPMLPKernels.metal:39-48, 164-173).
+ * mpp_mlp_f_h_f_n128 (a f32, taken as two f16 terms hi + lo, so f32 x half
+ * holds to ~2^-22 of each value) (MPPMLPKernels.metal:39-48, 164-173).
  * Any m, n >= 1; k % 32 == 0. */
 int mx_gemm_f16(mx_ctx* ctx, const void* a, int a_dtype, const void* b, float* c, int m, int n,
                 int k);

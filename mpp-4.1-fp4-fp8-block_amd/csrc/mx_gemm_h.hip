@@ -107,6 +107,8 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
   constexpr int MB = BM / 64;               // 32-row blocks per wave
   constexpr int ACH = A_F32 ? BM / 32 : BM / 64;  // A chunks per thread per step
   __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLdsRow];
+  // f32 activations: the second f16 term of each value, lo = f16(x - hi)
+  __shared__ __attribute__((aligned(16))) _Float16 Al[A_F32 ? 2 : 1][A_F32 ? BM * kLdsRow : 8];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][NB * kBN * kLdsRow];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -137,12 +139,15 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
   _Pragma("unroll") for (int c = 0; c < ACH; c++) {                                        \
     const int idx = tid + c * 256;                                                         \
     if (A_F32) {                                                                           \
-      v4h h;                                                                               \
-      h[0] = (_Float16)__builtin_bit_cast(float, areg[c].x);                               \
-      h[1] = (_Float16)__builtin_bit_cast(float, areg[c].y);                               \
-      h[2] = (_Float16)__builtin_bit_cast(float, areg[c].z);                               \
-      h[3] = (_Float16)__builtin_bit_cast(float, areg[c].w);                               \
+      const float x_[4] = {__builtin_bit_cast(float, areg[c].x), __builtin_bit_cast(float, areg[c].y), \
+                           __builtin_bit_cast(float, areg[c].z), __builtin_bit_cast(float, areg[c].w)}; \
+      v4h h, l;                                                                            \
+      _Pragma("unroll") for (int t = 0; t < 4; t++) {                                      \
+        h[t] = (_Float16)x_[t];                                                            \
+        l[t] = __builtin_isinf((float)h[t]) ? (_Float16)0.0f : (_Float16)(x_[t] - (float)h[t]); \
+      }                                                                                    \
       *reinterpret_cast<v4h*>(&As[buf][(idx >> 3) * kLdsRow + (idx & 7) * 4]) = h;         \
+      *reinterpret_cast<v4h*>(&Al[A_F32 ? buf : 0][(idx >> 3) * kLdsRow + (idx & 7) * 4]) = l; \
     } else {                                                                               \
       *reinterpret_cast<uint4*>(&As[buf][(idx >> 2) * kLdsRow + (idx & 3) * 8]) = areg[c]; \
     }                                                                                      \
@@ -192,6 +197,15 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
       for (int j = 0; j < NB; j++)
 #pragma unroll
         for (int i = 0; i < MB; i++) acc[j][i] = mfma_f16_32x32x16(af[i], bf[j], acc[j][i]);
+      if constexpr (A_F32 != 0) {  // the second term of the f32 activations
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+          const v8h al = *reinterpret_cast<const v8h*>(
+              &Al[buf][(wm * (BM / 2) + i * 32 + frag_row) * kLdsRow + ks * 16 + frag_k]);
+#pragma unroll
+          for (int j = 0; j < NB; j++) acc[j][i] = mfma_f16_32x32x16(al, bf[j], acc[j][i]);
+        }
+      }
     }
     MX_STORE_A(buf ^ 1)
     MX_STORE_B(buf ^ 1)

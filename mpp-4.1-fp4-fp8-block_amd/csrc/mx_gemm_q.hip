@@ -36,7 +36,8 @@
 //   decode    weights are widened in registers after the LDS read: FP4 with
 //             v_cvt_scalef32_pk_f16_fp4 (E8M0 applied), FP8 with
 //             v_cvt_scalef32_pk_f16_{fp8,bf8}, INT8 / INT4 with the 0x6400
-//             exponent trick, f32 activations with v_cvt_f16_f32.
+//             exponent trick; f32 activations as two f16 terms, hi = f16(x)
+//             and lo = f16(x - hi), two MFMAs (f32 x half kept to ~2^-22).
 //   split K   shapes with few tiles split K over gridDim.y; the partial tiles
 //             (f32, or i32 for W8A8) are summed in split order by a second
 //             kernel that also runs the epilogue, so results are deterministic.
@@ -562,16 +563,20 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
           _Pragma("unroll") for (int j = 0; j < NWB; j++)                                           \
             acc[i][j] = (AccT)__builtin_amdgcn_mfma_i32_32x32x32_i8(AR[s][i][0], BR[s][j], (v16i)acc[i][j], 0, 0, 0); \
       } else {                                                                                     \
-        v8h af[2], bf[NWB];                                                                        \
+        /* f32 activations: two f16 terms, x = hi + lo with lo = f16(x - hi) (0 where hi */      \
+        /* is infinite), so the sums keep f32 x times the f16 weights to ~2^-22 of x */            \
+        v8h af[2], afl[2], bf[NWB];                                                                \
         _Pragma("unroll") for (int i = 0; i < 2; i++) {                                            \
           if constexpr (AK == AK_F16) {                                                            \
             af[i] = __builtin_bit_cast(v8h, AR[s][i][0]);                                          \
           } else {                                                                                 \
-            const v4f lo_ = __builtin_bit_cast(v4f, AR[s][i][0]);                                  \
-            const v4f hi_ = __builtin_bit_cast(v4f, AR[s][i][AW - 1]);                             \
-            _Pragma("unroll") for (int t = 0; t < 4; t++) {                                        \
-              af[i][t] = (_Float16)lo_[t];                                                         \
-              af[i][4 + t] = (_Float16)hi_[t];                                                     \
+            const v4f p0_ = __builtin_bit_cast(v4f, AR[s][i][0]);                                  \
+            const v4f p1_ = __builtin_bit_cast(v4f, AR[s][i][AW - 1]);                             \
+            _Pragma("unroll") for (int t = 0; t < 8; t++) {                                        \
+              const float x_ = t < 4 ? p0_[t & 3] : p1_[t & 3];                                    \
+              const _Float16 h_ = (_Float16)x_;                                                    \
+              af[i][t] = h_;                                                                       \
+              afl[i][t] = __builtin_isinf((float)h_) ? (_Float16)0.0f : (_Float16)(x_ - (float)h_); \
             }                                                                                      \
           }                                                                                        \
         }                                                                                          \
@@ -591,8 +596,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
           }                                                                                        \
         }                                                                                          \
         _Pragma("unroll") for (int i = 0; i < 2; i++)                                              \
-          _Pragma("unroll") for (int j = 0; j < NWB; j++)                                           \
+          _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                         \
             acc[i][j] = (AccT)mfma_f16_32x32x16(af[i], bf[j], (v16f)acc[i][j]);                    \
+            if constexpr (AK == AK_F32) acc[i][j] = (AccT)mfma_f16_32x32x16(afl[i], bf[j], (v16f)acc[i][j]); \
+          }                                                                                        \
       }                                                                                            \
     }                                                                                              \
   }
