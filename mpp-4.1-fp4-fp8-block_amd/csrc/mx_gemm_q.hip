@@ -1270,10 +1270,13 @@ hipError_t launch_gemm_q(int ak, int bk, int epi, const QGemmArgs& g, hipStream_
   if (ak == AK_F16 && bk == BK_MXFP4 && small_gemm_ok(epi, g.m, g.n, g.k) &&
       ((reinterpret_cast<uintptr_t>(g.s0) | reinterpret_cast<uintptr_t>(g.s1)) & 3u) == 0)
     return launch_small_gemm(epi, g, st);
-  if (ak == AK_F16 && bk == BK_MXFP4 && kq_gemm_ok(epi, g.m, g.n, g.k) &&
+  // about one 64 x 64-channel gate/up tile per CU over a long K (C2): K
+  // split between the waves of a workgroup, no split-K partials
+  if (bk == BK_MXFP4 && kq_gemm_ok(ak, epi, g.m, g.n, g.k) &&
       ((reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b0) | reinterpret_cast<uintptr_t>(g.b1)) & 15u) == 0 &&
-      ((reinterpret_cast<uintptr_t>(g.s0) | reinterpret_cast<uintptr_t>(g.s1)) & 3u) == 0)
-    return launch_kq_gemm(epi, g, st);
+      ((reinterpret_cast<uintptr_t>(g.s0) | reinterpret_cast<uintptr_t>(g.s1) |
+        (ak == AK_F8X2 ? reinterpret_cast<uintptr_t>(g.a_e8) : 0)) & 3u) == 0)
+    return launch_kq_gemm(ak, epi, g, st);
   const int s = gemm_q_splits(ak, bk, epi, g.m, g.n, g.k);
   if (s > 1 && !g.ws) return hipErrorInvalidValue;
   if (ak == AK_I8) {

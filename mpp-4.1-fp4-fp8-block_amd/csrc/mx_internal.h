@@ -120,11 +120,12 @@ hipError_t launch_gemm_q(int akind, int bkind, int epi, const QGemmArgs& g, hipS
 bool small_gemm_ok(int epi, int m, int n, int k);
 hipError_t launch_small_gemm(int epi, const QGemmArgs& g, hipStream_t st);
 // K-split-in-workgroup MXFP4 gate/up + SwiGLU (mx_gemm_kq.hip): f16
-// activations, 64 x 64-channel tiles, 192 to 256 of them, K % 256 == 0 and
-// K >= 1024.  launch_gemm_q takes this path for the
-// AK_F16 x BK_MXFP4 SwiGLU shapes it accepts.
-bool kq_gemm_ok(int epi, int m, int n, int k);
-hipError_t launch_kq_gemm(int epi, const QGemmArgs& g, hipStream_t st);
+// activations (SwiGLU to f16) or F8X2 ones (SwiGLU to F8X2), 64 x 64-channel
+// tiles, 192 to 256 of them, K % 256 == 0 and K >= 1024 (BASELINE
+// configs[2]).  launch_gemm_q takes this path for the BK_MXFP4 shapes it
+// accepts.
+bool kq_gemm_ok(int ak, int epi, int m, int n, int k);
+hipError_t launch_kq_gemm(int ak, int epi, const QGemmArgs& g, hipStream_t st);
 // Grouped (MoE) form, MXFP4 weights and f16 activations only; g.m = the
 // largest group's rows, epi EPI_SWIGLU_F16 or EPI_STORE_F16, no split K.
 hipError_t launch_gemm_q_grouped(int epi, const QGemmArgs& g, const GroupTable& gt, int groups, hipStream_t st);

@@ -1,5 +1,6 @@
 """GPU parity of the MXFP4 gate/up GEMM that splits K inside a workgroup
-(mx_gemm_kq.hip).  launch_gemm_q takes it for f16 activations x MXFP4
+(mx_gemm_kq.hip).  launch_gemm_q takes it for f16 activations (fused and
+reference-row variants) and for F8X2 ones (the scaled variant) x MXFP4
 weights with a SwiGLU epilogue when the 64 x 64-channel tiles number 192 to
 256 and K % 256 == 0, K >= 1024: BASELINE configs[2] (T=512, H=7168,
 I=2048, also covered by test_config2_fused_and_dequant) and the shapes
@@ -90,4 +91,41 @@ def test_kq_nonfinite_x(dev):
     fin = np.isfinite(ref)
     rel, cos = O.mlp_error(got[fin], ref[fin])
     assert rel <= TOL and cos >= COS, (rel, cos)
+    d.free()
+
+
+@pytest.mark.parametrize("T,H,I", SHAPES)
+def test_kq_scaled(dev, T, H, I):
+    """The scaled variant (F8X2 x x FP4 on the scaled MFMA): BASELINE
+    tolerance against the oracle and 1e-2 of rms against the fused variant,
+    as the scaled rows are held elsewhere; deterministic."""
+    d = MlpData(dev, T, H, I, seed=350 + T)
+    got = run(dev, d, M.MLP_SCALED)
+    rel, cos = O.mlp_error(got, oracle(d, M.MLP_FUSED))
+    print(f"kq scaled T={T} H={H} I={I}: rel={rel:.3e} cos={cos:.7f}", flush=True)
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    rel2, cos2 = O.mlp_error(got, run(dev, d, M.MLP_FUSED).astype(np.float64))
+    assert rel2 <= 1e-2 and cos2 >= 0.99999, (rel2, cos2)
+    assert np.array_equal(run(dev, d, M.MLP_SCALED).view(np.uint16), got.view(np.uint16))
+    d.free()
+
+
+def test_kq_scaled_nonfinite_x(dev):
+    """Non-finite x in the scaled variant: its F8X2 groups carry scale bytes
+    255, and the mid values they reach are recomputed from the f16 x."""
+    T, H, I = 390, 1280, 2048
+    d = MlpData(dev, T, H, I, seed=361)
+    x = dev.download(d.x, np.float16, (T, H))
+    x[0, 5] = np.inf
+    x[T - 1, H - 3] = np.nan
+    x[200, 7] = -np.inf
+    dev.upload(x, d.x)
+    got = run(dev, d, M.MLP_SCALED).astype(np.float64)
+    ref = oracle(d, M.MLP_FUSED)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    rel, cos = O.mlp_error(got[fin], ref[fin])
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL, (rel, cos)
     d.free()

@@ -124,8 +124,10 @@ def _plant(dev, d, which):
 
 
 # (64, 512, 256): both GEMMs store from their own epilogue (no K split);
-# C0 (128, 1024, 4096): both split K, so the reduce kernels store.
-@pytest.mark.parametrize("T,H,I", [(64, 512, 256), (128, 1024, 4096)])
+# C0 (128, 1024, 4096): both split K, so the reduce kernels store;
+# (512, 1024, 2048): the gate/up GEMM splits K between the waves of one
+# workgroup per tile (mx_gemm_kq.hip) and recomputes in its own epilogue.
+@pytest.mark.parametrize("T,H,I", [(64, 512, 256), (128, 1024, 4096), (512, 1024, 2048)])
 @pytest.mark.parametrize("which", ["gate", "up", "down"])
 def test_scaled_e8m0_endpoints(dev, which, T, H, I):
     """E8M0 byte 255 is +inf to the reference (bits << 23,
