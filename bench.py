@@ -14,10 +14,11 @@ Secondary measurements (configs 0, 1 with T=8, 2, 3 and 4, and MoE grouped
 experts at the C1 and C2 expert shapes) are reported in
 the same JSON line under "secondary"; they are not the headline value.
 Each carries a "roofline" block for its longest GEMM/GEMV step (HBM for the
-decode GEMVs and the dequant kernels, the MFMA peak of the row's arithmetic
-otherwise: f16 for fp16-MFMA rows and for the scaled row, whose two FP8 x FP4
-MFMAs per block take the time of one f16 MFMA; FP4 for W4A4), or for the
-whole MLP where the library reports no per-step times (C3, MoE).
+decode GEMVs, the dequant kernels and the C3 weight-format GEMMs, the MFMA
+peak of the row's arithmetic otherwise: f16 for fp16-MFMA rows and for the
+scaled row, whose two FP8 x FP4 MFMAs per block take the time of one f16
+MFMA; FP4 for W4A4), or for the whole pass where the library reports no
+per-step times (MoE).
 
   value        effective TFLOP/s = 6*T*H*I / (time per step)
   roofline     the dominant kernel (fused gate/up GEMV): algorithmic bytes per
