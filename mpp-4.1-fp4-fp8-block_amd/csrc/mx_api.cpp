@@ -200,8 +200,10 @@ MlpScratch plan_scratch(int variant, const mx_mlp_config* cfg) {
     s.qws = take(std::max(q_ws(mx::AK_F16, mx::BK_F16, mx::EPI_STORE_F32, (int)T, (int)I, (int)H),
                           q_ws(mx::AK_F32, mx::BK_F16, mx::EPI_STORE_F16, (int)T, (int)H, (int)I)));
   } else if (variant == MX_MLP_W4A4) {
-    s.xq = take(T * H / 2);
-    s.mq = take(T * I / 2);
+    // stage-major codes (v6) take whole 256-row stage planes
+    const size_t Tc = mx::w4a4_act_stage_major((int)T, (int)H, (int)I) ? mx::stage_major_rows(T) : T;
+    s.xq = take(Tc * H / 2);
+    s.mq = take(Tc * I / 2);
     if (mx::w4a4_stage_major_ok((int)H, (int)I)) {
       // stage-major planes: [K/128][rows rounded up to 256] dwords
       const size_t Tp = mx::stage_major_rows(T);
@@ -340,10 +342,14 @@ int build_mlp_steps(mx_ctx* c, int variant, const mx_mlp_config* cfg, const void
       uint8_t* sg2 = ws + s.sg;
       uint8_t* su2 = ws + s.su;
       uint8_t* sd2 = ws + s.sd;
-      mx::W4A4Prologue pro{static_cast<const uint16_t*>(x), xq, xs, sg, su, sd, sg2, su2, sd2, T, H, I};
+      // Grids of whole tiles run both GEMMs on v6, which reads x and the mid
+      // stage-major as well.
+      const int asm_ = mx::w4a4_act_stage_major(T, H, I) ? 1 : 0;
+      mx::W4A4Prologue pro{static_cast<const uint16_t*>(x), xq, xs, sg, su, sd, sg2, su2, sd2, T, H, I, asm_};
       float* part = reinterpret_cast<float*>(ws + s.qws);
-      mx::Fp4GemmArgs gu{xq, xs, wg, sg2, wu, su2, mq, ms, T, I, H, 1, part, mx::gemm_fp4_splits(1, T, I, H)};
-      mx::Fp4GemmArgs dn{mq, ms, wd, sd2, nullptr, nullptr, out, nullptr, T, H, I, 1, part, mx::gemm_fp4_splits(0, T, H, I)};
+      mx::Fp4GemmArgs gu{xq, xs, wg, sg2, wu, su2, mq, ms, T, I, H, 1 + asm_, part, mx::gemm_fp4_splits(1, T, I, H)};
+      mx::Fp4GemmArgs dn{mq, ms, wd, sd2, nullptr, nullptr, out, nullptr, T, H, I, 1 + asm_, part,
+                         mx::gemm_fp4_splits(0, T, H, I)};
       steps.push_back({"w4a4_prologue", [=] { return mx::launch_w4a4_prologue(pro, st); }});
       steps.push_back({"gemm_fp4_gate_up_swiglu_requant", [=] { return mx::launch_gemm_fp4(1, gu, st); }});
       steps.push_back({"gemm_fp4_down", [=] { return mx::launch_gemm_fp4(0, dn, st); }});

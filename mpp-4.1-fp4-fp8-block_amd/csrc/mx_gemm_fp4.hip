@@ -347,6 +347,7 @@ hipError_t launch_w4a4_down_inf(const uint8_t* wd, const uint8_t* sd, const uint
 // Stage-major scale planes go to the 256 x 256 streaming kernel
 // (mx_gemm_fp4_v3.hip); reference-layout planes to the kernel above.
 hipError_t launch_gemm_fp4(int dual, const Fp4GemmArgs& g, hipStream_t st) {
+  if (g.stage_major == 2) return launch_gemm_fp4_v6(dual, g, st);
   if (g.stage_major) return gemm_fp4_v5_ok(g.k) ? launch_gemm_fp4_v5(dual, g, st) : launch_gemm_fp4_v3(dual, g, st);
   if (dual) return launch_bn<true, 128>(g, st);
   return launch_bn<false, 128>(g, st);

@@ -302,7 +302,10 @@ __global__ void k_w4a4_prologue(W4A4Prologue p, unsigned qb, int tiled) {
       o.z = fp4x8_from_f32(v + 16, sb);
       o.w = fp4x8_from_f32(v + 24, sb);
     }
-    reinterpret_cast<uint4*>(p.xq)[b] = o;
+    if (p.xq_sm)
+      *reinterpret_cast<uint4*>(p.xq + (((blk >> 2) * Tpad + row) << 6) + ((blk & 3) << 4)) = o;
+    else
+      reinterpret_cast<uint4*>(p.xq)[b] = o;
     p.xs[((blk >> 2) * Tpad + row) * 4 + (blk & 3)] = (uint8_t)sb;
     return;
   }

@@ -174,7 +174,9 @@ struct Fp4GemmArgs {
   void* c;                                // f16 [M][N] or mid MXFP4 [M][N/2]
   uint8_t* cs;                            // mid scales (dual epilogue)
   int m, n, k;
-  int stage_major;                        // 1: all scale planes stage-major
+  int stage_major;                        // 1: all scale planes stage-major; 2: also the
+                                          // activations and the dual epilogue's mid,
+                                          // [K/128][rows rounded up to 256][64 B] (v6)
   float* ws;                              // split-K partials (splits > 1)
   int splits;                             // K splits, from gemm_fp4_splits (0 or 1: none)
 };
@@ -188,6 +190,13 @@ hipError_t launch_gemm_fp4_v3(int dual_requant, const Fp4GemmArgs& g, hipStream_
 // Full-cache-line DMA, K stage 256 (mx_gemm_fp4_v5.hip), for K % 512 == 0.
 hipError_t launch_gemm_fp4_v5(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
 bool gemm_fp4_v5_ok(int k);
+// 128-K stages in a four-slot ring, stage-major activations
+// (mx_gemm_fp4_v6.hip), for whole-tile grids with K % 512 == 0.
+hipError_t launch_gemm_fp4_v6(int dual_requant, const Fp4GemmArgs& g, hipStream_t st);
+bool gemm_fp4_v6_ok(int dual_requant, int n, int k);
+// True when a W4A4 MLP (T x H x I) runs both GEMMs on v6, so that the
+// prologue writes x, and the gate/up GEMM the mid, stage-major.
+bool w4a4_act_stage_major(int t, int hidden, int inter);
 // True when the stage-major 256x256 kernel takes this MLP (T x H x I).
 bool w4a4_stage_major_ok(int hidden, int inter);
 __host__ __device__ inline size_t stage_major_rows(size_t rows) { return (rows + 255) / 256 * 256; }
@@ -198,6 +207,7 @@ struct W4A4Prologue {
   const uint8_t* sg; const uint8_t* su; const uint8_t* sd;   // reference layout
   uint8_t* sg2; uint8_t* su2; uint8_t* sd2;                  // stage-major
   int t, h, i;
+  int xq_sm;  // 1: x codes stage-major [H/128][Tpad][64 B], else [T][H/2]
 };
 hipError_t launch_w4a4_prologue(const W4A4Prologue& p, hipStream_t st);
 // After the W4A4 down GEMM: outputs of rows whose down scales hold byte 255

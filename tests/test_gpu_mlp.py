@@ -160,9 +160,12 @@ def test_mlp_dequant_small(dev, T):
 # Split-K of the down GEMM (f32 partials + reduce launch) on the stage-major
 # path: (64, 512, 1024) in 2 splits, (256, 1024, 2048) in 4, (130, 1024,
 # 4096) in 8 with a ragged last tile row, (400, 512, 2048) in 4 over two
-# row tiles (the second ragged).
+# row tiles (the second ragged).  Unsplit grids with H and I multiples of
+# 512 run both GEMMs on the 128-K-stage kernel with stage-major x and mid:
+# (300, 1024, 1536) with a ragged second row tile, (520, 1024, 1536) with
+# three row tiles (36 gate/up tiles, not a multiple of the 8 XCDs).
 @pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (256, 1024, 2048), (300, 768, 1536), (96, 640, 1152),
-                                   (130, 1024, 4096), (400, 512, 2048)])
+                                   (130, 1024, 4096), (400, 512, 2048), (300, 1024, 1536), (520, 1024, 1536)])
 def test_mlp_w4a4_small(dev, T, H, I):
     d = MlpData(dev, T, H, I, seed=200 + T)
     got = run_mlp(dev, d, M.MLP_W4A4)
@@ -452,10 +455,13 @@ def test_e8m0_endpoints_tiled_paths(dev, variant, which):
 
 
 # (64, 512, 1024): stage-major planes, the down GEMM split over K (its reduce
-# stores); (512, 2048, 512): the unsplit 256-K-stage down GEMM stores;
+# stores); (512, 2048, 512): the 128-K-stage kernel with stage-major x and
+# mid (gate/up epilogue and down stores); (300, 768, 1536): the unsplit
+# 256-K-stage down GEMM stores;
 # (64, 512, 640): the 128-K-stage down GEMM (K % 512 != 0) stores; (96, 640,
 # 1152): reference-layout planes with the separate byte-255 pass.
-@pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (512, 2048, 512), (64, 512, 640), (96, 640, 1152)])
+@pytest.mark.parametrize("T,H,I", [(64, 512, 1024), (512, 2048, 512), (300, 768, 1536), (64, 512, 640),
+                                   (96, 640, 1152)])
 @pytest.mark.parametrize("which", ["up", "down"])
 def test_e8m0_endpoints_w4a4(dev, T, H, I, which):
     """W4A4 (both scale layouts): byte 255 in an up scale makes the channel's

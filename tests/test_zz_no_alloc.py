@@ -22,6 +22,7 @@ CASES = [
     (M.MLP_REFROW, 512, 1024, 64, 3),
     (M.MLP_DEQUANT, 512, 1024, 130, 5),
     (M.MLP_W4A4, 1024, 2048, 256, 64),    # stage-major kernels, split-K down GEMM
+    (M.MLP_W4A4, 1024, 1536, 300, 44),    # 128-K-stage kernels, stage-major x and mid
     (M.MLP_W4A4, 640, 1152, 96, 17),      # reference scale layout
     (M.MLP_SCALED, 1024, 2048, 128, 9),   # split of x, F8X2 mid, split-K reduce
 ]
