@@ -156,9 +156,11 @@ def make_sets(dev, M, T, H, I, n_sets, seed, wfmt=0):
 
 
 def run_config(dev, M, name, variant, T, H, I, n_sets, iters, warmup, seed, wfmt=0, cpu=None, cpu_flop_cap=1e11):
-    """Time `iters` forwards twice: replayed from one HIP graph (the value;
-    the reference likewise pre-encodes all iterations in one command buffer)
-    and launched one by one on the stream (reported as stream_us_per_iter).
+    """Time `iters` forwards twice: replayed from one HIP graph, between
+    timing events that are the graph's first and last nodes (the value; the
+    reference likewise pre-encodes all iterations in one command buffer and
+    reports its GPU start-to-end time, main.swift:2062-2133), and launched one
+    by one on the stream (reported as stream_us_per_iter).
     cpu: None, or the token count of the CPU baseline sample run on this
     row's own inputs (weight set 0) before they are freed."""
     x, sets, bufs = make_sets(dev, M, T, H, I, n_sets, seed, wfmt)

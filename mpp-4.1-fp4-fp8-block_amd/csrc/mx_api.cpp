@@ -810,16 +810,25 @@ const char* mx_mlp_kernel_name(int variant, const mx_mlp_config* cfg, int index)
   return nullptr;
 }
 
-// Capture `iterations` forwards into one HIP graph (kernel nodes only: no
-// memset or copy nodes) - the counterpart of the reference encoding all
-// iterations into one command buffer (main.swift:2062-2117).
+// Capture `iterations` forwards into one HIP graph (kernel nodes and the two
+// timing events only: no memset or copy nodes) - the counterpart of the
+// reference encoding all iterations into one command buffer
+// (main.swift:2062-2117).  `start` / `end` are recorded as the graph's first
+// and last nodes, so their interval is the graph's execution on the GPU, as
+// the reference reports gpuEndTime - gpuStartTime (main.swift:2131-2133).
 static int capture_graph(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int iterations,
-                         hipGraphExec_t* exec) {
+                         hipGraphExec_t* exec, hipEvent_t start, hipEvent_t end) {
   const int ns = (int)sets.size();
   hipGraph_t graph = nullptr;
   MX_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
   int rc = MX_OK;
+  // hipEventRecordExternal: captured as event record nodes of the graph
+  // (a plain record inside a capture only orders captured work)
+  if (hipEventRecordWithFlags(start, c->stream, hipEventRecordExternal) != hipSuccess)
+    rc = set_err(c, MX_EGPU, "event record failed");
   for (int i = 0; i < iterations && !rc; i++) rc = run_steps(c, sets[i % ns]);
+  if (!rc && hipEventRecordWithFlags(end, c->stream, hipEventRecordExternal) != hipSuccess)
+    rc = set_err(c, MX_EGPU, "event record failed");
   hipError_t e = hipStreamEndCapture(c->stream, &graph);
   if (rc) { if (graph) (void)hipGraphDestroy(graph); return rc; }
   if (e != hipSuccess) return set_err(c, MX_EGPU, "graph capture failed: %s", hipGetErrorString(e));
@@ -830,47 +839,46 @@ static int capture_graph(mx_ctx* c, const std::vector<std::vector<Step>>& sets, 
 }
 
 // Time `iterations` passes over `sets` (set i % n_sets on pass i) between two
-// events: replayed from one captured graph, or launched one by one.  When
-// there are more sets than passes, the sets the timed passes do not use run
-// once (untimed) just before the timed region, so that what the timed passes
-// read was evicted from the last-level cache by at least that many bytes.
+// events: replayed from one captured graph (events inside it, around its
+// kernels), or launched one by one (events on the stream around the
+// launches).  When there are more sets than passes, the sets the timed
+// passes do not use run once (untimed) just before the timed region, so that
+// what the timed passes read was evicted from the last-level cache by at
+// least that many bytes.
 static int time_passes(mx_ctx* c, const std::vector<std::vector<Step>>& sets, int iterations,
                        int use_graph, double* seconds) {
   const int ns = (int)sets.size();
-  hipGraphExec_t gexec = nullptr;
-  if (use_graph) {
-    if (int rc = capture_graph(c, sets, iterations, &gexec)) return rc;
-    // one untimed replay (first launch of an instantiated graph uploads it)
-    if (hipGraphLaunch(gexec, c->stream) != hipSuccess) {
-      (void)hipGraphExecDestroy(gexec);
-      return set_err(c, MX_EGPU, "graph launch failed");
-    }
-  }
-  for (int i = iterations; i < ns; i++) {
-    if (int rc = run_steps(c, sets[(size_t)i])) {
-      if (gexec) (void)hipGraphExecDestroy(gexec);
-      return rc;
-    }
-  }
   hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    if (e0) (void)hipEventDestroy(e0);
+    return set_err(c, MX_EGPU, "event create failed");
+  }
+  hipGraphExec_t gexec = nullptr;
   int rc = MX_OK;
+  if (use_graph) {
+    rc = capture_graph(c, sets, iterations, &gexec, e0, e1);
+    // one untimed replay (first launch of an instantiated graph uploads it)
+    if (!rc && hipGraphLaunch(gexec, c->stream) != hipSuccess) rc = set_err(c, MX_EGPU, "graph launch failed");
+  }
+  for (int i = iterations; i < ns && !rc; i++) rc = run_steps(c, sets[(size_t)i]);
   do {
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-      rc = set_err(c, MX_EGPU, "event create failed");
-      break;
-    }
+    if (rc) break;
     if (hipStreamSynchronize(c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "sync failed"); break; }
-    if (hipEventRecord(e0, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
     if (gexec) {
       if (hipGraphLaunch(gexec, c->stream) != hipSuccess) rc = set_err(c, MX_EGPU, "graph launch failed");
     } else {
+      if (hipEventRecord(e0, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
       for (int i = 0; i < iterations && !rc; i++) rc = run_steps(c, sets[i % ns]);
+      if (!rc && hipEventRecord(e1, c->stream) != hipSuccess) rc = set_err(c, MX_EGPU, "event record failed");
     }
     if (rc) break;
-    if (hipEventRecord(e1, c->stream) != hipSuccess) { rc = set_err(c, MX_EGPU, "event record failed"); break; }
     if (hipEventSynchronize(e1) != hipSuccess) { rc = set_err(c, MX_EGPU, "MXFP4 MLP timed loop failed."); break; }
     float ms = 0.0f;
-    (void)hipEventElapsedTime(&ms, e0, e1);
+    const hipError_t te = hipEventElapsedTime(&ms, e0, e1);
+    if (te != hipSuccess || !(ms > 0.0f)) {
+      rc = set_err(c, MX_EGPU, "timing events gave no interval: %s", hipGetErrorString(te));
+      break;
+    }
     *seconds = ms / 1000.0;
   } while (0);
   if (e0) (void)hipEventDestroy(e0);
