@@ -72,9 +72,12 @@ __device__ __forceinline__ uint8_t* ring() {
   else return ring3;
 }
 
-// Chunk swizzle of a 64-byte row (depends on row % 32 only): within any 8
-// or 16 consecutive rows, (row % 2, swz) resp. (row % 4, swz) are distinct.
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// Chunk swizzle of a 64-byte row (depends on row % 32 only).  Chosen by
+// measurement: with it SQ_LDS_BANK_CONFLICT is 0 for both C4 GEMMs; so it
+// is with (row >> 2) & 3 or (row ^ (row >> 2)) & 3, while ((row >> 1) ^
+// (row >> 3)) & 3, (row >> 1) & 3 and ((row >> 2) ^ (row >> 4)) & 3 left
+// 2.5 conflict cycles per LDS instruction (and no swizzle 7.5).
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 3; }
 
 // s_waitcnt immediate (gfx9 encoding): lgkmcnt(0), expcnt untouched, vmcnt(n).
 constexpr int wait_lgkm0_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
