@@ -238,6 +238,14 @@ constexpr int kScLds = 16384;
 constexpr int sc_lds_bytes(int ak, int ns = 2) {
   return ns == 4 ? 49152 : ak == AK_F8X2 ? kScLds - 2048 : kScLds;
 }
+// Row stride of the LDS scale copy: the row's bytes rounded up to dwords,
+// plus a dword when that count is even.  A stage's scales are read at one
+// offset from 32 consecutive rows, and an odd dword stride spreads them over
+// distinct banks.  The unpadded 64-byte rows (16 dwords) of C2's down GEMM
+// measured 5 bank-conflict cycles per LDS instruction (SQ_LDS_BANK_CONFLICT).
+constexpr int sc_ld_bytes(int row_bytes) {
+  return ((row_bytes + 3) / 4 + (((row_bytes + 3) / 4) % 2 == 0 ? 1 : 0)) * 4;
+}
 template <int AK, int BK, int EPI, int NWB, bool GROUPED, int BCH, int NS = 2, bool SCL = false, bool SCW = false>
 __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     QGemmArgs g, typename std::conditional<GROUPED, GroupTable, int>::type grp) {
@@ -376,6 +384,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   constexpr int ESZ = BK == BK_INT4G32 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint8_t sc_lds[SCL ? sc_lds_bytes(AK, NS) : 16];
   const int sc_row = KT * (KS / 32) * ESZ;  // bytes of one row's scales
+  const int sc_ld = sc_ld_bytes(sc_row);     // their LDS row stride
   const bool sc_dma =                       // workgroup-uniform
       SCL && sc_row % 4 == 0 && (K / 32 * ESZ) % 4 == 0 && (kt0 * (KS / 32) * ESZ) % 4 == 0;
   if constexpr (SCL) {
@@ -386,16 +395,19 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       return sb + ((size_t)wrow * (K / 32) + (size_t)kt0 * (KS / 32)) * ESZ + byte;
     };
     if (sc_dma) {
-      const int dws = TBR * sc_row / 4;
+      // LDS dword i: row i / (sc_ld / 4), dword i % (sc_ld / 4); the pad
+      // dword re-reads the row's first one
+      const int dws = TBR * sc_ld / 4;
       for (int i0 = wave * 64; i0 < dws; i0 += 256) {  // wave-uniform
         const int i = i0 + lane;
-        if (i < dws) dma4(src_of(i / (sc_row / 4), (i % (sc_row / 4)) * 4), sc_lds + (size_t)i0 * 4);
+        const int c = i % (sc_ld / 4);
+        if (i < dws) dma4(src_of(i / (sc_ld / 4), c < sc_row / 4 ? c * 4 : 0), sc_lds + (size_t)i0 * 4);
       }
     } else {
       const int units = TBR * sc_row / 2;
       for (int i = tid; i < units; i += 256) {
         const int tr = i / (sc_row / 2), c = i % (sc_row / 2);
-        *reinterpret_cast<uint16_t*>(sc_lds + tr * sc_row + c * 2) =
+        *reinterpret_cast<uint16_t*>(sc_lds + tr * sc_ld + c * 2) =
             *reinterpret_cast<const uint16_t*>(src_of(tr, c * 2));
       }
       __syncthreads();
@@ -420,7 +432,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   {                                                                                                \
     if constexpr (SCL) {                                                                           \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
-        const uint8_t* p_ = sc_lds + (b_blk[j] + r32) * sc_row + ((S) * (KS / 32) + h) * ESZ;     \
+        const uint8_t* p_ = sc_lds + (b_blk[j] + r32) * sc_ld + ((S) * (KS / 32) + h) * ESZ;      \
         scv[P][j] = ESZ == 2 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_;  \
       }                                                                                            \
     } else if (SCALES4 && !SCW) {                                                                  \
@@ -1062,7 +1074,7 @@ template <int AK, int BK> constexpr int b_chunk() {
 
 // True when a workgroup's scales over kt stages fit the LDS copy (SCL).
 template <int AK, int BK, int NWB, int NS = 2> bool sc_lds_fits(int kt) {
-  return NWB * 64 * kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1) <= sc_lds_bytes(AK, NS);
+  return NWB * 64 * sc_ld_bytes(kt * (AInfo<AK>::KS / 32) * (BK == BK_INT4G32 ? 2 : 1)) <= sc_lds_bytes(AK, NS);
 }
 
 // True when the chunk scale loads (SCW) are aligned: every row's scales, the
