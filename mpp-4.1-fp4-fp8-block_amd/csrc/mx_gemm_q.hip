@@ -681,6 +681,20 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   //      a repeated copy, never used), then stage st's MFMAs.
 #define MXQ_AS(i) ((i) == 0 ? d_s0 : (i) == 1 ? d_s1 : (i) == 2 ? d_s2 : d_s3)
 #define MXQ_BS(i) (MXQ_AS(i) + kTM * RA)
+  // Stage body of the deep ring: refill slot st, read stage st+1's
+  // fragments, stage st's math.  Issued as a block ahead of the MFMAs, the
+  // DMAs and reads took about 320 cycles per 64-K stage at C2's down GEMM
+  // (timed with s_memtime in a copy), with no MFMA running.  F8X2 stages
+  // issue them between the MFMAs instead (C2's scaled down GEMM 21.3-21.7 ->
+  // 18.8-19.0 us, same box).  Measured and not kept for the other forms:
+  // the same interleave with the weight decode made C2's fused down GEMM
+  // 25.7 -> 30.5 us (the decode pushed the next stage's reads behind the
+  // MFMAs) and left the 8-bit formats unchanged.
+#define MXQ_DEEP_ISSUE(U, NXT, PC)                                                                 \
+  MXQ_DMA_A(min(st_ + NS, KT - 1), MXQ_AS(U))                                                      \
+  MXQ_DMA_B(min(st_ + NS, KT - 1), MXQ_BS(U))                                                      \
+  MXQ_READ(MXQ_AS(((U) + 1) % NS), MXQ_BS(((U) + 1) % NS), 0, NXT##_a, NXT##_b)                    \
+  if constexpr (SCALES4) MXQ_SCALES(min(st_ + 1, KT - 1), (PC) ^ 1)
 #define MXQ_DEEP(U, CUR, NXT)                                                                      \
   {                                                                                                \
     const int st_ = kt + (U);                                                                      \
@@ -692,13 +706,33 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     else __builtin_amdgcn_s_waitcnt(wait_vm((NS - 2) * VM_A) & ~(15 << 8));                        \
     __builtin_amdgcn_s_barrier();                                                                  \
     __builtin_amdgcn_sched_barrier(0);                                                             \
-    MXQ_DMA_A(min(st_ + NS, KT - 1), MXQ_AS(U))                                                    \
-    MXQ_DMA_B(min(st_ + NS, KT - 1), MXQ_BS(U))                                                    \
-    MXQ_READ(MXQ_AS(((U) + 1) % NS), MXQ_BS(((U) + 1) % NS), 0, NXT##_a, NXT##_b)                  \
-    if constexpr (SCALES4) MXQ_SCALES(min(st_ + 1, KT - 1), PC_ ^ 1)                               \
-    __builtin_amdgcn_sched_barrier(0);                                                             \
-    MXQ_MATH(CUR##_a, CUR##_b, PC_)                                                                \
+    MXQ_DEEP_ISSUE(U, NXT, PC_)                                                                    \
+    if constexpr (AK == AK_F8X2) {                                                                 \
+      MXQ_MATH_F8X2(CUR##_a, CUR##_b, PC_)                                                         \
+      _Pragma("unroll") for (int q_ = 0; q_ < DEEP_VM; q_++) {                                     \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                         \
+        __builtin_amdgcn_sched_group_barrier(0x100, DEEP_DS, 0);                                   \
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                         \
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                         \
+      }                                                                                            \
+      _Pragma("unroll") for (int q_ = DEEP_VM; q_ < DEEP_MF; q_++) {                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                         \
+        __builtin_amdgcn_sched_group_barrier(0x100, DEEP_DS, 0);                                   \
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                         \
+      }                                                                                            \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+    } else {                                                                                       \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+      MXQ_MATH(CUR##_a, CUR##_b, PC_)                                                              \
+    }                                                                                              \
   }
+  // F8X2 stages of the deep ring interleave the DMAs and the next stage's
+  // reads with the MFMAs: per MFMA, DEEP_DS LDS reads, one DMA while they
+  // last, and up to four VALU instructions (the operand packing).
+  constexpr int DEEP_MF = 2 * NWB * 2;
+  constexpr int DEEP_NDS = KSTEPS * 2 * AW + BREADS * NWB + (SCALES4 ? NWB : 0) + 2;
+  constexpr int DEEP_DS = (DEEP_NDS + DEEP_MF - 1) / DEEP_MF;
+  constexpr int DEEP_VM = VM_A + NB;
   if constexpr (NS > 2) {
     static_assert(NS == 4 && (NS - 1) * (VM_A + NB) <= 63, "vmcnt range");
     v4i f0_a[KSTEPS][2][AW], f1_a[KSTEPS][2][AW];
@@ -755,6 +789,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   }
   }
 #undef MXQ_DEEP
+#undef MXQ_DEEP_ISSUE
 #undef MXQ_AS
 #undef MXQ_BS
 #undef MXQ_BODY
