@@ -414,6 +414,26 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     }
   }
 
+  // ONE_FORM: MXFP4 weights with f16 / f32 activations whose scales are all
+  // in the LDS copy run the whole K loop in one byte-255 form, chosen by one
+  // scan of the copy (sc_any255, once the copy has landed: a 0xff byte
+  // anywhere picks the exact form for every stage).
+  constexpr bool ONE_FORM = SCL && BK == BK_MXFP4 && AK != AK_F8X2;
+  auto sc_any255 = [&]() -> bool {
+    if constexpr (!ONE_FORM) {
+      return false;
+    } else {
+      uint32_t hit = 0;
+      for (int i = lane * 16; i < TBR * sc_ld; i += 64 * 16) {  // TBR * sc_ld: a multiple of 256
+        const uint4 v = *reinterpret_cast<const uint4*>(sc_lds + i);
+        const uint32_t d[4] = {~v.x, ~v.y, ~v.z, ~v.w};  // a 0xff byte becomes a zero byte
+#pragma unroll
+        for (int t = 0; t < 4; t++) hit |= (d[t] - 0x01010101u) & ~d[t] & 0x80808080u;
+      }
+      return __ballot(hit != 0) != 0;
+    }
+  };
+
   // SCW: chunk scales by chunk parity, SCWD dwords per row (chunk C's
   // element e of the lane's row is at byte e * ESZ of the chunk's bytes).
   constexpr int SCWD = SCW ? BCH * (KS / 32) * ESZ / 4 : 1;
@@ -554,9 +574,18 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       }                                                                                            \
     }                                                                                              \
   }
+  // EXF_: the byte-255 form of every stage of the loop in scope (0 fast, 1
+  // exact), or 2: decided per stage.  A per-stage branch made the compiler
+  // copy all accumulators between the two forms' registers at every stage
+  // (64 v_accvgpr_mov per stage at C2's down GEMM); loops over a workgroup
+  // whose scales are all in LDS decide once, from one scan of the copy.
 #define MXQ_MATH(AR, BR, P)                                                                        \
   if constexpr (AK == AK_F8X2) {                                                                   \
     MXQ_MATH_F8X2(AR, BR, P)                                                                       \
+  } else if constexpr (EXF_ == 0) {                                                                \
+    MXQ_MATH_FORM(AR, BR, P, false)                                                                \
+  } else if constexpr (EXF_ == 1) {                                                                \
+    MXQ_MATH_FORM(AR, BR, P, true)                                                                 \
   } else {                                                                                         \
     bool exact_ = false;                                                                           \
     if constexpr (BK == BK_MXFP4) {                                                                \
@@ -746,11 +775,22 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     else __builtin_amdgcn_s_waitcnt(wait_vm((NS - 1) * VM_A));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    const bool any255 = sc_any255();
+    __builtin_amdgcn_sched_barrier(0);
     MXQ_READ(MXQ_AS(0), MXQ_BS(0), 0, f0_a, f0_b)
     if constexpr (SCALES4) MXQ_SCALES(0, 0)
     __builtin_amdgcn_sched_barrier(0);
-    for (int kt = 0; kt < KT; kt += NS) {
-      MXQ_DEEP(0, f0, f1) MXQ_DEEP(1, f1, f0) MXQ_DEEP(2, f0, f1) MXQ_DEEP(3, f1, f0)
+    auto deep_loop = [&](auto exf) {
+      constexpr int EXF_ = decltype(exf)::value;
+      for (int kt = 0; kt < KT; kt += NS) {
+        MXQ_DEEP(0, f0, f1) MXQ_DEEP(1, f1, f0) MXQ_DEEP(2, f0, f1) MXQ_DEEP(3, f1, f0)
+      }
+    };
+    if constexpr (ONE_FORM) {
+      if (__builtin_expect(any255, 0)) deep_loop(std::integral_constant<int, 1>{});
+      else deep_loop(std::integral_constant<int, 0>{});
+    } else {
+      deep_loop(std::integral_constant<int, 2>{});
     }
   } else {
   MXQ_DMA_A(0, a_s0)
@@ -763,7 +803,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   }
+  const bool any255 = sc_any255();
   MXQ_SCALES(0, 0)
+  auto ring2_loop = [&](auto exf) {
+  constexpr int EXF_ = decltype(exf)::value;
   if constexpr (BCH == 1) {
     int kt = 0;
     for (; kt + 2 <= KT; kt += 2) {
@@ -786,6 +829,13 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       MXQ_BODY(0) MXQ_BODY(1) MXQ_BODY(2) MXQ_BODY(3)
       MXQ_BODY(4) MXQ_BODY(5) MXQ_BODY(6) MXQ_BODY(7)
     }
+  }
+  };
+  if constexpr (ONE_FORM) {
+    if (__builtin_expect(any255, 0)) ring2_loop(std::integral_constant<int, 1>{});
+    else ring2_loop(std::integral_constant<int, 0>{});
+  } else {
+    ring2_loop(std::integral_constant<int, 2>{});
   }
   }
 #undef MXQ_DEEP
