@@ -713,12 +713,13 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // Stage body of the deep ring: refill slot st, read stage st+1's
   // fragments, stage st's math.  Issued as a block ahead of the MFMAs, the
   // DMAs and reads took about 320 cycles per 64-K stage at C2's down GEMM
-  // (timed with s_memtime in a copy), with no MFMA running.  F8X2 stages
-  // issue them between the MFMAs instead (C2's scaled down GEMM 21.3-21.7 ->
-  // 18.8-19.0 us, same box).  Measured and not kept for the other forms:
-  // the same interleave with the weight decode made C2's fused down GEMM
-  // 25.7 -> 30.5 us (the decode pushed the next stage's reads behind the
-  // MFMAs) and left the 8-bit formats unchanged.
+  // (timed with s_memtime in a copy), with no MFMA running.  F8X2 stages,
+  // and MXFP4 stages under f16 activations in a loop of the fast byte-255
+  // form, issue them between the MFMAs instead (same box: C2's scaled down
+  // GEMM 21.3-21.7 -> 18.8-19.0 us, C2's fused down GEMM 22.1-22.2 -> 19.6-
+  // 20.2 us).  Measured and not kept: the interleave inside the per-stage
+  // byte-255 branch (fused down 25.7 -> 30.5 us) and for the 8-bit formats
+  // (unchanged).
 #define MXQ_DEEP_ISSUE(U, NXT, PC)                                                                 \
   MXQ_DMA_A(min(st_ + NS, KT - 1), MXQ_AS(U))                                                      \
   MXQ_DMA_B(min(st_ + NS, KT - 1), MXQ_BS(U))                                                      \
@@ -736,18 +737,18 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     __builtin_amdgcn_s_barrier();                                                                  \
     __builtin_amdgcn_sched_barrier(0);                                                             \
     MXQ_DEEP_ISSUE(U, NXT, PC_)                                                                    \
-    if constexpr (AK == AK_F8X2) {                                                                 \
-      MXQ_MATH_F8X2(CUR##_a, CUR##_b, PC_)                                                         \
+    if constexpr (AK == AK_F8X2 || (EXF_ == 0 && AK == AK_F16)) {                                  \
+      MXQ_MATH(CUR##_a, CUR##_b, PC_)                                                              \
       _Pragma("unroll") for (int q_ = 0; q_ < DEEP_VM; q_++) {                                     \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                         \
         __builtin_amdgcn_sched_group_barrier(0x100, DEEP_DS, 0);                                   \
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                         \
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                         \
+        if constexpr (DEEP_VALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, DEEP_VALU, 0);    \
       }                                                                                            \
       _Pragma("unroll") for (int q_ = DEEP_VM; q_ < DEEP_MF; q_++) {                               \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                         \
         __builtin_amdgcn_sched_group_barrier(0x100, DEEP_DS, 0);                                   \
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                         \
+        if constexpr (DEEP_VALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, DEEP_VALU, 0);    \
       }                                                                                            \
       __builtin_amdgcn_sched_barrier(0);                                                           \
     } else {                                                                                       \
@@ -755,11 +756,14 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
       MXQ_MATH(CUR##_a, CUR##_b, PC_)                                                              \
     }                                                                                              \
   }
-  // F8X2 stages of the deep ring interleave the DMAs and the next stage's
-  // reads with the MFMAs: per MFMA, DEEP_DS LDS reads, one DMA while they
-  // last, and up to four VALU instructions (the operand packing).
-  constexpr int DEEP_MF = 2 * NWB * 2;
-  constexpr int DEEP_NDS = KSTEPS * 2 * AW + BREADS * NWB + (SCALES4 ? NWB : 0) + 2;
+  // Interleaved deep-ring stages (F8X2 activations; MXFP4 weights under f16
+  // activations in the fast byte-255 form): per MFMA, DEEP_DS LDS reads, one
+  // DMA while they last, and for F8X2 up to four VALU instructions (the
+  // operand packing; the f16 form leaves its decode to the scheduler, which
+  // measured 2 us faster at C2's down GEMM than four VALU per MFMA).
+  constexpr int DEEP_MF = AK == AK_F8X2 ? 2 * NWB * 2 : 2 * NWB * KSTEPS;
+  constexpr int DEEP_NDS = KSTEPS * 2 * AW + BREADS * NWB + (SCALES4 ? NWB : 0) + (AK == AK_F8X2 ? 2 : 0);
+  constexpr int DEEP_VALU = AK == AK_F8X2 ? 4 : 0;
   constexpr int DEEP_DS = (DEEP_NDS + DEEP_MF - 1) / DEEP_MF;
   constexpr int DEEP_VM = VM_A + NB;
   if constexpr (NS > 2) {
