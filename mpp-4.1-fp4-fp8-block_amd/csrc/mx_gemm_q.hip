@@ -714,12 +714,15 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // fragments, stage st's math.  Issued as a block ahead of the MFMAs, the
   // DMAs and reads took about 320 cycles per 64-K stage at C2's down GEMM
   // (timed with s_memtime in a copy), with no MFMA running.  F8X2 stages,
-  // and MXFP4 stages under f16 activations in a loop of the fast byte-255
-  // form, issue them between the MFMAs instead (same box: C2's scaled down
-  // GEMM 21.3-21.7 -> 18.8-19.0 us, C2's fused down GEMM 22.1-22.2 -> 19.6-
-  // 20.2 us).  Measured and not kept: the interleave inside the per-stage
-  // byte-255 branch (fused down 25.7 -> 30.5 us) and for the 8-bit formats
-  // (unchanged).
+  // and stages under f16 activations (MXFP4 weights in a loop of the fast
+  // byte-255 form, or 8-bit weights), issue them between the MFMAs instead.
+  // Same box: C2's scaled down GEMM 21.3-21.7 -> 18.8-19.0 us, C2's fused
+  // down GEMM 22.1-22.2 -> 19.6-20.2 us, C3's FP8 / INT8 gate/up GEMMs
+  // 46.2-46.5 -> 40.4-41.6 / 48.2-49.8 -> 43.5-44.1 us.  Measured and not
+  // kept: the interleave inside the per-stage byte-255 branch (fused down
+  // 25.7 -> 30.5 us), and with four VALU instructions per MFMA in the
+  // pattern for f16 activations (8-bit rows unchanged, fused down 2 us
+  // slower).
 #define MXQ_DEEP_ISSUE(U, NXT, PC)                                                                 \
   MXQ_DMA_A(min(st_ + NS, KT - 1), MXQ_AS(U))                                                      \
   MXQ_DMA_B(min(st_ + NS, KT - 1), MXQ_BS(U))                                                      \
@@ -737,7 +740,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
     __builtin_amdgcn_s_barrier();                                                                  \
     __builtin_amdgcn_sched_barrier(0);                                                             \
     MXQ_DEEP_ISSUE(U, NXT, PC_)                                                                    \
-    if constexpr (AK == AK_F8X2 || (EXF_ == 0 && AK == AK_F16)) {                                  \
+    if constexpr (DEEP_IL) {                                                                       \
       MXQ_MATH(CUR##_a, CUR##_b, PC_)                                                              \
       _Pragma("unroll") for (int q_ = 0; q_ < DEEP_VM; q_++) {                                     \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                         \
@@ -764,6 +767,9 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   constexpr int DEEP_MF = AK == AK_F8X2 ? 2 * NWB * 2 : 2 * NWB * KSTEPS;
   constexpr int DEEP_NDS = KSTEPS * 2 * AW + BREADS * NWB + (SCALES4 ? NWB : 0) + (AK == AK_F8X2 ? 2 : 0);
   constexpr int DEEP_VALU = AK == AK_F8X2 ? 4 : 0;
+  // which loops interleave: F8X2; f16 activations with MXFP4 weights in the
+  // fast byte-255 loop (EXF_ 0) or with 8-bit weights (no byte-255 forms)
+#define DEEP_IL (AK == AK_F8X2 || (AK == AK_F16 && (EXF_ == 0 || (BK != BK_MXFP4 && BK != BK_INT4G32))))
   constexpr int DEEP_DS = (DEEP_NDS + DEEP_MF - 1) / DEEP_MF;
   constexpr int DEEP_VM = VM_A + NB;
   if constexpr (NS > 2) {
@@ -844,6 +850,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   }
 #undef MXQ_DEEP
 #undef MXQ_DEEP_ISSUE
+#undef DEEP_IL
 #undef MXQ_AS
 #undef MXQ_BS
 #undef MXQ_BODY
