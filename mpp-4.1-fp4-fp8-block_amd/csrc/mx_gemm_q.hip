@@ -718,7 +718,8 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // byte-255 form, or 8-bit weights), issue them between the MFMAs instead.
   // Same box: C2's scaled down GEMM 21.3-21.7 -> 18.8-19.0 us, C2's fused
   // down GEMM 22.1-22.2 -> 19.6-20.2 us, C3's FP8 / INT8 gate/up GEMMs
-  // 46.2-46.5 -> 40.4-41.6 / 48.2-49.8 -> 43.5-44.1 us.  Measured and not
+  // 46.2-46.5 -> 40.4-41.6 / 48.2-49.8 -> 43.5-44.1 us, C3's W8A8 gate/up
+  // 33.2-33.4 -> 32.8 us.  Measured and not
   // kept: the interleave inside the per-stage byte-255 branch (fused down
   // 25.7 -> 30.5 us), and with four VALU instructions per MFMA in the
   // pattern for f16 activations (8-bit rows unchanged, fused down 2 us
@@ -767,9 +768,10 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   constexpr int DEEP_MF = AK == AK_F8X2 ? 2 * NWB * 2 : 2 * NWB * KSTEPS;
   constexpr int DEEP_NDS = KSTEPS * 2 * AW + BREADS * NWB + (SCALES4 ? NWB : 0) + (AK == AK_F8X2 ? 2 : 0);
   constexpr int DEEP_VALU = AK == AK_F8X2 ? 4 : 0;
-  // which loops interleave: F8X2; f16 activations with MXFP4 weights in the
-  // fast byte-255 loop (EXF_ 0) or with 8-bit weights (no byte-255 forms)
-#define DEEP_IL (AK == AK_F8X2 || (AK == AK_F16 && (EXF_ == 0 || (BK != BK_MXFP4 && BK != BK_INT4G32))))
+  // which loops interleave: F8X2; int8 activations (W8A8); f16 activations
+  // with MXFP4 weights in the fast byte-255 loop (EXF_ 0) or with 8-bit
+  // weights (no byte-255 forms)
+#define DEEP_IL (AK == AK_F8X2 || AK == AK_I8 || (AK == AK_F16 && (EXF_ == 0 || (BK != BK_MXFP4 && BK != BK_INT4G32))))
   constexpr int DEEP_DS = (DEEP_NDS + DEEP_MF - 1) / DEEP_MF;
   constexpr int DEEP_VM = VM_A + NB;
   if constexpr (NS > 2) {
