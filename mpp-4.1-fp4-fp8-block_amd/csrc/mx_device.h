@@ -56,7 +56,16 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// silu(g) = g / (1 + e^-g) for the f16 and F8X2 mids of the fused rows, the
+// W4A4 mid and the decode GEMV: g times the hardware reciprocal (v_rcp_f32)
+// of 1 + 2^(-g log2 e) (v_exp_f32), about 1 ulp of f32 from the IEEE
+// quotient, below the f16 / FP8 / FP4 rounding of the mid, and with the same
+// special values (-inf -> NaN, large negative g -> -0, +inf -> +inf, NaN ->
+// NaN).  Five VALU instructions against about twenty for the IEEE form,
+// which cost ~1 us of a gate/up GEMM's epilogue at one wave per SIMD.  The
+// f32 mid of W8A8 (re-quantized to int8, bit-exact against the oracle) and
+// the reference-row SwiGLU (swiglu_half) keep the IEEE form.
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // Two FP4 codes (byte `sel` of `src`) -> two halves, each fp4 * 2^(scale-127).
 template <int SEL>

@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void k_gemm_h(GemmArgs g) {
         float u = acc[NB - 1][i][v] * rs1;
         float m;
         if (EPI == EPI_SWIGLU_F16) {
-          m = (x0 / (1.0f + expf(-x0))) * u;
+          m = silu(x0) * u;
         } else {
           float gg = fminf(fmaxf(x0 * 0.0625f, -20.0f), 20.0f);
           m = (gg / (1.0f + expf(-gg))) * (u * 0.0625f);

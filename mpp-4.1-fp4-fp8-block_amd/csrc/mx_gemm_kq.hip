@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_kq_gate_up(QGemmArgs g) {
           const float gg = fminf(fmaxf(gs[e] * 0.0625f, -20.0f), 20.0f);
           mv = (gg / (1.0f + expf(-gg))) * (us[e] * 0.0625f);
         } else {
-          mv = (gs[e] / (1.0f + expf(-gs[e]))) * us[e];
+          mv = silu(gs[e]) * us[e];
         }
         const int row = 32 * i + acc32_row(ln, 4 * vq + e);
         if constexpr (F8) tile32[row * 64 + 32 * jg + (ln & 31)] = mv;

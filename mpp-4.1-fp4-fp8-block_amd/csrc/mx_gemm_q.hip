@@ -153,7 +153,7 @@ __device__ __forceinline__ void epi_store(void* c, size_t o, float x0, float u) 
   } else if (EPI == EPI_SWIGLU_F32) {
     reinterpret_cast<float*>(c)[o] = (x0 / (1.0f + expf(-x0))) * u;
   } else if (EPI == EPI_SWIGLU_F16) {
-    reinterpret_cast<uint16_t*>(c)[o] = f32_to_f16_bits((x0 / (1.0f + expf(-x0))) * u);
+    reinterpret_cast<uint16_t*>(c)[o] = f32_to_f16_bits(silu(x0) * u);
   } else {  // EPI_SWIGLU_HALF: silu(clamp(g/16, +-20)) * u/16 (MPPMLPKernels.metal:204-220)
     const float gg = fminf(fmaxf(x0 * 0.0625f, -20.0f), 20.0f);
     reinterpret_cast<uint16_t*>(c)[o] = f32_to_f16_bits((gg / (1.0f + expf(-gg))) * (u * 0.0625f));
@@ -934,7 +934,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
         const int rl = i * 32 + acc32_row(lane, v), c = wn * 32 + r32;
         float x0 = acc[i][0][v], u = acc[i][NWB - 1][v];
         if (row_scaled(BK)) { x0 = x0 * csg; u = u * csu; }
-        ml[rl * 64 + (c ^ (rl & 31))] = (x0 / (1.0f + expf(-x0))) * u;
+        ml[rl * 64 + (c ^ (rl & 31))] = silu(x0) * u;
       }
     __syncthreads();
     const int pr = tid >> 1, half = tid & 1, rl = pr & 63;
@@ -1091,7 +1091,7 @@ __global__ void k_gemm_q_reduce(QGemmArgs g, int splits) {
       const int ch = grp * 64 + 4 * j + c;
       const float gg = row_scaled(BK) ? gs[c] * row_scale<BK>(g.s0, ch) : gs[c];
       const float uu = row_scaled(BK) ? us[c] * row_scale<BK>(g.s1, ch) : us[c];
-      mv[c] = (gg / (1.0f + expf(-gg))) * uu;
+      mv[c] = silu(gg) * uu;
     }
     // non-finite mid (E8M0 byte 255 in a gate / up scale, or a non-finite x):
     // recomputed from the f16 activations with the reference's dequantization

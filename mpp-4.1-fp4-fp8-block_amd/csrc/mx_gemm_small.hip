@@ -220,7 +220,7 @@ __global__ __launch_bounds__(512) void k_small_gate_up(QGemmArgs g) {
       const float gg = fminf(fmaxf(t[0] * 0.0625f, -20.0f), 20.0f);
       mv = silu_f(gg) * (t[1] * 0.0625f);
     } else {
-      mv = silu_f(t[0]) * t[1];
+      mv = silu(t[0]) * t[1];
     }
     tile[acc32_row(lane, v) * 64 + cb * 32 + j] = f32_to_f16_bits(mv);
   }
