@@ -440,24 +440,43 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   static_assert(!SCW || SCWD == 2 || SCWD == 4, "8- or 16-byte chunk scale loads");
   uint32_t scw[2][NWB][SCWD];
 
+  // Deep ring, gate/up launches: loop stage S reads K stage MXQ_PS(S) =
+  // (S + krot) mod KT.  All workgroups of such a launch read the same
+  // activation lines of a stage, 8 KB or more apart; started in step, the
+  // 28 workgroups of an XCD (workgroup ids 8 apart) request them from the
+  // same few L2 channels at once.  Workgroup w starts at stage 7 (w / 8) mod
+  // KT instead, which spreads an XCD's workgroups over distinct stages.  A
+  // read probe of C3's gate/up pattern (224 workgroups, 128 weight rows and
+  // 128 x 64 activations per stage): 38.7 -> 33.5 us per pass.  Same box,
+  // three alternating runs: C3's W8A8 gate/up 35.1-35.5 -> 31.1-31.6 us,
+  // its F8X2 gate/up 42.4-43.3 -> 41.7-41.8 us, FP8 / INT8 within noise.
+  // Down GEMMs keep the in-step order: their activation lines are shared by
+  // only the four workgroups of an XCD with the same split, and the rotated
+  // order measured 2-5 us slower on C3's down GEMMs (fewer L2 hits).  Only
+  // the f32 summation order of a tile changes.
+  int krot = 0;
+  if constexpr (NS > 2 && DUAL) krot = (int)(blockIdx.x + blockIdx.y * gridDim.x) / 8 * 7 % KT;
+#define MXQ_PS(S) ((S) + krot >= KT ? (S) + krot - KT : (S) + krot)
+
   // A of stage S into slot AS; the 4-bit scales of stage S into register set P.
 #define MXQ_DMA_A(S, AS)                                                                           \
   {                                                                                                \
-    const size_t ka_ = (size_t)(kt0 + (S)) * RA;                                                   \
+    const int ps_ = MXQ_PS(S);                                                                     \
+    const size_t ka_ = (size_t)(kt0 + ps_) * RA;                                                   \
     _Pragma("unroll") for (int q = 0; q < NA; q++)                                                 \
       dma16(a_src[q] + ka_, (AS) + (wave * NA + q) * 1024);                                         \
-    if constexpr (AK == AK_F8X2) dma4(ae_src + (size_t)(kt0 + (S)) * M, (AS) + ASC + wave * 256);  \
+    if constexpr (AK == AK_F8X2) dma4(ae_src + (size_t)(kt0 + ps_) * M, (AS) + ASC + wave * 256);  \
   }
 #define MXQ_SCALES(S, P)                                                                           \
   {                                                                                                \
     if constexpr (SCL) {                                                                           \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
-        const uint8_t* p_ = sc_lds + (b_blk[j] + r32) * sc_ld + ((S) * (KS / 32) + h) * ESZ;      \
+        const uint8_t* p_ = sc_lds + (b_blk[j] + r32) * sc_ld + (MXQ_PS(S) * (KS / 32) + h) * ESZ; \
         scv[P][j] = ESZ == 2 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_;  \
       }                                                                                            \
     } else if (SCALES4 && !SCW) {                                                                  \
       _Pragma("unroll") for (int j = 0; j < NWB; j++) {                                             \
-        const uint8_t* p_ = sc_src[j] + (size_t)(S) * (KS / 32) * (BK == BK_INT4G32 ? 2 : 1);     \
+        const uint8_t* p_ = sc_src[j] + (size_t)MXQ_PS(S) * (KS / 32) * (BK == BK_INT4G32 ? 2 : 1); \
         scv[P][j] = BK == BK_INT4G32 ? (uint32_t)*reinterpret_cast<const uint16_t*>(p_) : (uint32_t)*p_; \
       }                                                                                            \
     }                                                                                              \
@@ -488,7 +507,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   // B chunk C (stages C*BCH .. C*BCH + BCH - 1) into slot BS.
 #define MXQ_DMA_B(C, BS)                                                                         \
   {                                                                                                \
-    const size_t kb_ = (size_t)(kt0 + (C) * BCH) * RB;                                             \
+    const size_t kb_ = (size_t)(kt0 + MXQ_PS((C) * BCH)) * RB; /* krot is 0 for chunked B */       \
     if (b_issuer) {                                                                                \
       _Pragma("unroll") for (int q = 0; q < NB; q++) {                                             \
         const int qi_ = NBC >= 4 ? wave * NB + q : wave;                                           \
@@ -862,6 +881,7 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
 #undef MXQ_DMA_A
 #undef MXQ_DMA_B
 #undef MXQ_SCALES
+#undef MXQ_PS
 #undef MXQ_SCW_LOAD
 #undef MXQ_SCW_PICK
 #undef MXQ_COMPUTE
