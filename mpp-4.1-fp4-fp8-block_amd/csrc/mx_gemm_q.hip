@@ -788,9 +788,11 @@ __global__ __launch_bounds__(256, NS == 2 ? 2 : 1) void k_gemm_q(
   constexpr int DEEP_NDS = KSTEPS * 2 * AW + BREADS * NWB + (SCALES4 ? NWB : 0) + (AK == AK_F8X2 ? 2 : 0);
   constexpr int DEEP_VALU = AK == AK_F8X2 ? 4 : 0;
   // which loops interleave: F8X2; int8 activations (W8A8); f16 activations
-  // with MXFP4 weights in the fast byte-255 loop (EXF_ 0) or with 8-bit
-  // weights (no byte-255 forms)
-#define DEEP_IL (AK == AK_F8X2 || AK == AK_I8 || (AK == AK_F16 && (EXF_ == 0 || (BK != BK_MXFP4 && BK != BK_INT4G32))))
+  // with MXFP4 weights in the fast byte-255 loop (EXF_ 0), or with 8-bit or
+  // INT4 weights (no byte-255 forms).  INT4's decode (17 VALU per 8 values)
+  // is left to the scheduler too: eight VALU per MFMA in the pattern
+  // measured 1-2 us slower on C3's INT4 gate/up.
+#define DEEP_IL (AK == AK_F8X2 || AK == AK_I8 || (AK == AK_F16 && (EXF_ == 0 || BK != BK_MXFP4)))
   constexpr int DEEP_DS = (DEEP_NDS + DEEP_MF - 1) / DEEP_MF;
   constexpr int DEEP_VM = VM_A + NB;
   if constexpr (NS > 2) {
@@ -1213,14 +1215,19 @@ template <int AK, int BK> bool scw_ok(const QGemmArgs& g, bool dual, size_t s_st
 // (not f32 activations x f16 weights: 4 x 48 KB).  MXFP4 weights under f16
 // activations take it too, with their E8M0 scales in LDS beside the ring
 // (80 KB + up to 48 KB) when those fit, for splits of at least 16 stages
-// (C2's down GEMM, 224 workgroups: 27.4 -> 24.4 us).
+// (C2's down GEMM, 224 workgroups: 27.4 -> 24.4 us).  INT4 g32 weights do
+// the same with their f16 scales, for gate/up launches only: on the
+// interleaved ring C3's INT4 gate/up went 53.1-54.0 -> 49.9-51.1 us (same
+// box, three alternating runs), while its down GEMM (64 tiles x 4 splits
+// there) went 32.0-33.7 -> 35.7-36.2 us and keeps the 2-slot ring.
 constexpr int kDeepMaxWgs = 256;
 constexpr bool deep_format(int ak, int bk) {
   const int ks = ak == AK_I8 ? 128 : 64;
   const int ra = ak == AK_F32 ? 256 : 128;
   const int rb = bk == BK_F16 ? ks * 2 : ks;
   if (bk == BK_MXFP4) return ak == AK_F16 || ak == AK_F8X2;
-  return bk != BK_INT4G32 && 4 * 128 * (ra + rb) <= 160 * 1024;
+  if (bk == BK_INT4G32) return ak == AK_F16;  // gate/up launches only (launch_q)
+  return 4 * 128 * (ra + rb) <= 160 * 1024;
 }
 
 // Workgroups of the split-K reduction: 4 outputs per thread (16 lanes per
@@ -1241,11 +1248,11 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   // keeps the host and device kernel-argument layouts identical)
   // chunked B once a split spans at least four chunks (a shorter split would
   // wait for its whole B up front)
-  if constexpr (deep_format(AK, BK)) {
+  if constexpr (deep_format(AK, BK) && (BK != BK_INT4G32 || is_dual(EPI))) {
     // MXFP4: scales in LDS, and at least 16 stages (C0's 8-stage splits
     // measured 1 us slower per GEMM on the deep ring: its fill and drain
     // are not repaid)
-    constexpr bool S4D = BK == BK_MXFP4;
+    constexpr bool S4D = BK == BK_MXFP4 || BK == BK_INT4G32;
     if (g.tiles_m * tiles_n * splits <= kDeepMaxWgs && kt >= 8 && kt % 4 == 0 &&
         (!S4D || (kt >= 16 && sc_lds_fits<AK, BK, NWB, 4>(kt)))) {
       hipLaunchKernelGGL((k_gemm_q<AK, BK, EPI, NWB, false, 1, 4, S4D>), dim3(g.tiles_m * tiles_n, splits), dim3(256),
