@@ -92,6 +92,19 @@ def test_format_mlp_small(dev, wfmt, T):
 
 
 @pytest.mark.parametrize("wfmt", MLP_FMTS)
+def test_format_mlp_deep_ragged(dev, wfmt):
+    """Gate/up on the deep ring (K = 1024: 16 stages; 2 x 32 tiles), a
+    ragged second token tile, and per-workgroup start stages that wrap
+    (7 (w / 8) mod 16)."""
+    d = MlpData(dev, 130, 1024, 2048, seed=53 + wfmt, wfmt=wfmt)
+    got = run_fmt(dev, d, wfmt)
+    rel, cos = O.mlp_error(got, oracle_fmt(d, wfmt))
+    print(f"fmt {wfmt} T=130 H=1024 I=2048: rel={rel:.3e} cos={cos:.7f}", flush=True)
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    d.free()
+
+
+@pytest.mark.parametrize("wfmt", MLP_FMTS)
 def test_config3_formats(dev, wfmt):
     d = MlpData(dev, 128, 4096, 14336, seed=31 + wfmt, wfmt=wfmt)
     rows = sample_rows(128, 16)
@@ -103,10 +116,12 @@ def test_config3_formats(dev, wfmt):
 
 
 def test_int4_scale_planes_4_byte_aligned(dev):
-    """INT4 gate/up GEMM with 224 tiles and 32 KB of f16 scales per
-    workgroup: 16-byte aligned planes load a B chunk's scales with one
-    16-byte load per lane, planes at a 4-byte offset one scale per stage.
-    Same output bits."""
+    """INT4 scale planes at a 4-byte offset against 16-byte aligned ones,
+    same output bits.  The gate/up GEMM (224 tiles, deep ring) copies its
+    32 KB of f16 scales per workgroup to LDS by dword DMA either way; the
+    down GEMM (2-slot ring, scales not in LDS) loads a B chunk's scales
+    with one 16-byte load per lane from aligned planes and one scale per
+    stage from shifted ones."""
     T, H, I = 32, 4096, 14336
     d = MlpData(dev, T, H, I, seed=41, wfmt=M.WFMT_INT4)
     ref = run_fmt(dev, d, M.WFMT_INT4)
