@@ -255,21 +255,39 @@ __device__ __forceinline__ void ld_src4(const void* p, size_t base, int c, float
 }
 
 // One workgroup (512 threads) per row: amax (wave shuffles, one barrier),
-// scale = amax / qmax, then every element v / scale to the format.  The row
-// is read twice (the second pass from cache), 4 elements per load.
+// scale = amax / qmax, then every element v / scale to the format, 4
+// elements per load.  Rows of at most 512 x 8 chunks (k <= 16384) keep the
+// thread's chunks in registers between the two passes: all of a thread's
+// loads are in flight at once and the row is read once.  Longer rows are
+// read twice (the second pass from cache).
 template <bool SRC_F16>
 __global__ __launch_bounds__(512) void k_quant_rowwise(int fmt, const void* __restrict__ w, int k,
                                                        uint8_t* __restrict__ q, float* __restrict__ row_scale) {
+  constexpr int RCH = 8;  // chunks per thread kept in registers
   __shared__ float red[8];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const size_t base = (size_t)row * k;
   const int nch = k / 4;
+  const bool in_regs = nch <= 512 * RCH;  // workgroup-uniform
+  float v[RCH][4];
   float amax = 0.0f;
-  for (int c = tid; c < nch; c += 512) {
-    float v[4];
-    ld_src4<SRC_F16>(w, base, c, v);
+  if (in_regs) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) amax = fmaxf(amax, fabsf(v[t]));
+    for (int i = 0; i < RCH; i++) {
+      if (tid + 512 * i < nch) ld_src4<SRC_F16>(w, base, tid + 512 * i, v[i]);
+      else v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < RCH; i++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) amax = fmaxf(amax, fabsf(v[i][t]));
+  } else {
+    for (int c = tid; c < nch; c += 512) {
+      float u[4];
+      ld_src4<SRC_F16>(w, base, c, u);
+#pragma unroll
+      for (int t = 0; t < 4; t++) amax = fmaxf(amax, fabsf(u[t]));
+    }
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
@@ -282,23 +300,29 @@ __global__ __launch_bounds__(512) void k_quant_rowwise(int fmt, const void* __re
   const float sc = amax > 0.0f ? amax / qmax : 1.0f;
   if (tid == 0) row_scale[row] = sc;
   uint32_t* dst = reinterpret_cast<uint32_t*>(q + base);
-  for (int c = tid; c < nch; c += 512) {
-    float v[4];
-    ld_src4<SRC_F16>(w, base, c, v);
-    const float v0 = v[0] / sc, v1 = v[1] / sc, v2 = v[2] / sc, v3 = v[3] / sc;
-    uint32_t r;
-    if (fmt == 1) r = fp8x4_from_f32<false>(v0, v1, v2, v3);
-    else if (fmt == 2) r = fp8x4_from_f32<true>(v0, v1, v2, v3);
-    else {
-      float vv[4] = {v0, v1, v2, v3};
-      r = 0;
+  auto quant4 = [&](const float u[4]) -> uint32_t {
+    const float v0 = u[0] / sc, v1 = u[1] / sc, v2 = u[2] / sc, v3 = u[3] / sc;
+    if (fmt == 1) return fp8x4_from_f32<false>(v0, v1, v2, v3);
+    if (fmt == 2) return fp8x4_from_f32<true>(v0, v1, v2, v3);
+    const float vv[4] = {v0, v1, v2, v3};
+    uint32_t r = 0;
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        float rv = fminf(fmaxf(rintf(vv[t]), -127.0f), 127.0f);
-        r |= ((uint32_t)(int)rv & 0xffu) << (8 * t);
-      }
+    for (int t = 0; t < 4; t++) {
+      const float rv = fminf(fmaxf(rintf(vv[t]), -127.0f), 127.0f);
+      r |= ((uint32_t)(int)rv & 0xffu) << (8 * t);
     }
-    dst[c] = r;
+    return r;
+  };
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < RCH; i++)
+      if (tid + 512 * i < nch) dst[tid + 512 * i] = quant4(v[i]);
+  } else {
+    for (int c = tid; c < nch; c += 512) {
+      float u[4];
+      ld_src4<SRC_F16>(w, base, c, u);
+      dst[c] = quant4(u);
+    }
   }
 }
 
