@@ -1216,17 +1216,18 @@ template <int AK, int BK> bool scw_ok(const QGemmArgs& g, bool dual, size_t s_st
 // activations take it too, with their E8M0 scales in LDS beside the ring
 // (80 KB + up to 48 KB) when those fit, for splits of at least 16 stages
 // (C2's down GEMM, 224 workgroups: 27.4 -> 24.4 us).  INT4 g32 weights do
-// the same with their f16 scales, for gate/up launches only: on the
-// interleaved ring C3's INT4 gate/up went 53.1-54.0 -> 49.9-51.1 us (same
-// box, three alternating runs), while its down GEMM (64 tiles x 4 splits
-// there) went 32.0-33.7 -> 35.7-36.2 us and keeps the 2-slot ring.
+// the same with their f16 scales.  Same box, three alternating runs: C3's
+// INT4 gate/up 53.1-54.0 -> 49.9-51.1 us; its down GEMM, as 32 tiles of 128
+// rows x 8 splits on the deep ring against 64 tiles of 64 rows x 8 splits
+// on the 2-slot ring, 30.2-30.4 -> 29.3-29.4 us (MLP 75.3-75.4 -> 73.0-73.4
+// us, stream-timed).
 constexpr int kDeepMaxWgs = 256;
 constexpr bool deep_format(int ak, int bk) {
   const int ks = ak == AK_I8 ? 128 : 64;
   const int ra = ak == AK_F32 ? 256 : 128;
   const int rb = bk == BK_F16 ? ks * 2 : ks;
   if (bk == BK_MXFP4) return ak == AK_F16 || ak == AK_F8X2;
-  if (bk == BK_INT4G32) return ak == AK_F16;  // gate/up launches only (launch_q)
+  if (bk == BK_INT4G32) return ak == AK_F16;
   return 4 * 128 * (ra + rb) <= 160 * 1024;
 }
 
@@ -1248,7 +1249,7 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
   // keeps the host and device kernel-argument layouts identical)
   // chunked B once a split spans at least four chunks (a shorter split would
   // wait for its whole B up front)
-  if constexpr (deep_format(AK, BK) && (BK != BK_INT4G32 || is_dual(EPI))) {
+  if constexpr (deep_format(AK, BK)) {
     // MXFP4: scales in LDS, and at least 16 stages (C0's 8-stage splits
     // measured 1 us slower per GEMM on the deep ring: its fill and drain
     // are not repaid)
@@ -1282,17 +1283,18 @@ hipError_t launch_q(const QGemmArgs& g0, int splits, hipStream_t st) {
 }
 
 // Plain (non-SwiGLU) GEMMs take 128-row weight tiles when N allows, except
-// MXFP4 with fewer than 16 of them and INT4 with fewer than 64: 64-row tiles
-// then give the grid twice the tiles (C0's down GEMM, N = 1024: 13.5 ->
-// 12.6 us per step with its reduce, 12.25 -> 11.5 us on the F8X2 path; C3
-// INT4's down GEMM, N = 4096: the MLP 96.8 -> 94.1 us in stream mode).
-// Other formats measured no gain (C3) or a loss (C2 dequant, f16 weights:
-// +2.5 us).  C2's MXFP4 down GEMM on 64-row tiles (448 two-slot workgroups
+// MXFP4 with fewer than 16 of them: 64-row tiles then give the grid twice
+// the tiles (C0's down GEMM, N = 1024: 13.5 -> 12.6 us per step with its
+// reduce, 12.25 -> 11.5 us on the F8X2 path).  INT4 took 64-row tiles below
+// 64 wide tiles while it ran on the 2-slot ring only (C3's down GEMM, N =
+// 4096: MLP 96.8 -> 94.1 us then); on the deep ring its 128-row tiles halve
+// the activation re-reads and measured faster (launch_q's note).  Other
+// formats measured no gain (C3) or a loss (C2 dequant, f16 weights: +2.5
+// us).  C2's MXFP4 down GEMM on 64-row tiles (448 two-slot workgroups
 // instead of 224 on the deep ring): fused 23.6 -> 24.9 us; scaled 20.2 ->
 // 18.7 us but the scaled MLP unchanged (66.1-67.1 against 67.0-67.3 us).
 inline bool wide_tiles(int bk, int epi, int n) {
-  return !is_dual(epi) && n % 128 == 0 && !(bk == BK_MXFP4 && n / 128 < 16) &&
-         !(bk == BK_INT4G32 && n / 128 < 64);
+  return !is_dual(epi) && n % 128 == 0 && !(bk == BK_MXFP4 && n / 128 < 16);
 }
 
 template <int AK, int BK, int EPI>
