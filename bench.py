@@ -158,7 +158,7 @@ def make_sets(dev, M, T, H, I, n_sets, seed, wfmt=0):
 SPINUP_S = 0.3  # untimed forwards before each row's timed region (wall-clock seconds)
 
 
-def spin_up(call, iters, seconds=SPINUP_S):
+def spin_up(call, iters, seconds=None):
     """Bring the GPU to steady state before a timed region: untimed
     stream-mode passes of the row's own forwards, in calls of at least ~50 ms
     of GPU work, for `seconds` of wall time.  `call(n)` runs n forwards and
@@ -167,6 +167,9 @@ def spin_up(call, iters, seconds=SPINUP_S):
     the first four measurements; stream-mode timing likewise settled at
     69-70 us.  A row measured first after process start or after the host
     work of a CPU baseline otherwise reports the GPU's ramp."""
+    seconds = SPINUP_S if seconds is None else seconds
+    if seconds <= 0:
+        return
     t0 = time.time()
     per = call(iters) / iters
     n = max(iters, int(0.05 / max(per, 1e-7)))
@@ -350,12 +353,16 @@ def measured_traffic(kernel):
 
 
 def main():
+    global SPINUP_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--spinup", type=float, default=SPINUP_S,
+                    help="seconds of untimed forwards before each row's timed region (0: none; "
+                         "profiler runs, whose tracer records every dispatch)")
     ap.add_argument("--only", default="",
                     help="comma-separated secondary configs to run (c1_t8,c4,c0,c2,c3,moe), or one variant "
                          "of a config (c0_fused, c2_dequant, c3_int8, ...); default all")
@@ -366,6 +373,7 @@ def main():
     if args.copy_probe:
         copy_probe()
         return
+    SPINUP_S = args.spinup
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
               "(the MXFP4 MLP hot path here is a single-GPU kernel; a multi-GPU run would shard "
