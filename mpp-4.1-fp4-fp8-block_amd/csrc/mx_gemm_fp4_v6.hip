@@ -325,23 +325,30 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v6(Fp4GemmArgs g) {
   if (!DUAL) {
     uint16_t* c = reinterpret_cast<uint16_t*>(g.c);
     uint64_t nanm[4] = {0u, 0u, 0u, 0u};  // bit j * 16 + v of word i: element is NaN
+    // The wave's 128 x 128 outputs go to its own ring slot as an f16 tile
+    // (row pitch 136 halves: the slot's 34816 B), then out as 16-byte
+    // stores, 16 lanes per 256-byte row, where the accumulator layout gives
+    // 256 two-byte stores per lane.  Same box, three alternating runs at
+    // C4: down GEMM 401.5-402.8 -> 398.5-402.0 us.  The epilogue's ~10 us
+    // per tile is mostly the write burst: 256 CUs store their 128 KB tiles
+    // at the same time.  The W4A4 MLP entry points require 16-byte aligned
+    // outputs (mx_api.cpp), and N is a whole number of 256-column tiles.
+    uint16_t* tile = reinterpret_cast<uint16_t*>(wave == 0 ? ring<0>() : wave == 1 ? ring<1>() : wave == 2 ? ring<2>() : ring<3>());
+    constexpr int kPitch = 136;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int col = nt * 256 + (wn * 4 + j) * 32 + r32;
+      for (int j = 0; j < 4; j++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-          const int row = m0 + wm * 128 + i * 32 + acc32_row(lane, v);
           const float x0 = acc[i][j][v];
           nanm[i] |= (uint64_t)(x0 != x0) << (j * 16 + v);
-          if (row < M) c[(size_t)row * g.n + col] = f32_to_f16_bits(x0);
+          tile[(i * 32 + acc32_row(lane, v)) * kPitch + j * 32 + r32] = f32_to_f16_bits(x0);
         }
-      }
     // E8M0 byte 255 in a scale is NaN to the scaled MFMA and +inf to the
     // reference (MXFP4Kernels.metal:26-29), whose dequantize-then-accumulate
     // gives +-inf or NaN there: NaN outputs (rare; one wave-uniform test)
-    // are recomputed with the reference's dequantization.
+    // are recomputed with the reference's dequantization, into the tile.
     if (__builtin_expect(__ballot((nanm[0] | nanm[1] | nanm[2] | nanm[3]) != 0) != 0, 0)) {
 #pragma nounroll
       for (int e = 0; e < 256; e++) {
@@ -350,8 +357,18 @@ __global__ __launch_bounds__(256, 1) void k_gemm_fp4_v6(Fp4GemmArgs g) {
         const int row = m0 + wm * 128 + i * 32 + acc32_row(lane, v);
         const int col = nt * 256 + (wn * 4 + j) * 32 + r32;
         if (row < M)
-          c[(size_t)row * g.n + col] = f32_to_f16_bits(ref_dot_sm_a(g.a, g.as, Mpad, row, g.b0, g.s0, NB, col, K));
+          tile[(i * 32 + acc32_row(lane, v)) * kPitch + j * 32 + r32] =
+              f32_to_f16_bits(ref_dot_sm_a(g.a, g.as, Mpad, row, g.b0, g.s0, NB, col, K));
       }
+    }
+    __syncthreads();  // the tile's elements were written by other lanes of the wave
+#pragma unroll 4
+    for (int q = 0; q < 32; q++) {
+      const int id = q * 64 + lane, r = id >> 4, ch = id & 15;
+      const int row = m0 + wm * 128 + r;
+      if (row < M)
+        *reinterpret_cast<uint4*>(c + (size_t)row * g.n + nt * 256 + wn * 128 + ch * 8) =
+            *reinterpret_cast<const uint4*>(tile + r * kPitch + ch * 8);
     }
     return;
   }
