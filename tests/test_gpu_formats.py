@@ -104,6 +104,20 @@ def test_format_mlp_deep_ragged(dev, wfmt):
     d.free()
 
 
+@pytest.mark.parametrize("wfmt", [M.WFMT_FP8_E4M3, M.WFMT_INT8])
+def test_format_mlp_deep_kt12(dev, wfmt):
+    """Gate/up on the deep ring with 12 stages (K = 768) over 192 tiles:
+    start stages 7 (w / 8) mod 12 take every residue, so the wrap of the
+    rotated K order is exercised away from a power of two."""
+    d = MlpData(dev, 128, 768, 12288, seed=61 + wfmt, wfmt=wfmt)
+    rows = sample_rows(128, 16)
+    got = run_fmt(dev, d, wfmt)[rows]
+    rel, cos = O.mlp_error(got, oracle_fmt(d, wfmt, rows=rows))
+    print(f"fmt {wfmt} T=128 H=768 I=12288: rel={rel:.3e} cos={cos:.7f}", flush=True)
+    assert rel <= O.MAX_ABS_REL_TOL and cos >= O.COSINE_TOL
+    d.free()
+
+
 @pytest.mark.parametrize("wfmt", MLP_FMTS)
 def test_config3_formats(dev, wfmt):
     d = MlpData(dev, 128, 4096, 14336, seed=31 + wfmt, wfmt=wfmt)
